@@ -1,0 +1,322 @@
+"""Benchmark of the quantized-weight hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+
+Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
+x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
+workloads under "workloads": Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
+(4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096) and the Q4_0 MoE
+grouped GEMM (128 experts, 64 tokens, top-8).
+
+Measurement
+  - Inputs are synthetic and seeded, converted to the planar layout and
+    resident in HBM before timing. Every workload cycles through enough
+    copies of its weights to exceed the 256 MB Infinity Cache twice over, so
+    successive launches read HBM, not the last-level cache.
+  - A "step" is one launch of the workload's kernel(s). W warm-up steps, then
+    K steps captured in a HIP graph and replayed once between two
+    synchronizations: whole-job time -> "ms_per_step" and "value".
+  - Kernel duration for the roofline: the same K launches run eagerly with a
+    HIP event pair around each launch on the launch stream, queued behind a
+    spin kernel so that the CPU is ahead of the GPU; the mean of the pairs.
+  - "roofline.achieved" is algorithmic bytes (or FLOPs) per launch divided by
+    that mean. "traffic" comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter
+    runs recorded in profiles/traffic.json when present.
+  - "cpu_baseline": the CPU oracle's streaming dequantize-and-multiply over the
+    same canonical Q8_0 tensor, on the host's cores, repeated for ~10 s.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA
+LLC_BYTES = 256 << 20        # Infinity Cache
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", default=None, help="run one workload (for profiling)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def copies_for(bytes_per_step):
+    return max(2, int(np.ceil(2 * LLC_BYTES / bytes_per_step)))
+
+
+class Timer:
+    def __init__(self, torch):
+        self.torch = torch
+
+    def run(self, launch, steps, warmup):
+        torch = self.torch
+        stream = torch.cuda.current_stream()
+        for i in range(warmup):
+            launch(i)
+        torch.cuda.synchronize()
+        # Whole-job: K launches in one graph, replayed once.
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                launch(i)
+        g.replay()  # first replay uploads the graph
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        g.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        # Kernel duration: per-launch event pairs queued behind a spin kernel.
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        torch.cuda._sleep(int(2e7))
+        for i in range(steps):
+            starts[i].record(stream)
+            launch(i)
+            ends[i].record(stream)
+        torch.cuda.synchronize()
+        durs = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)]) * 1e-3  # seconds
+        del g
+        return wall, durs
+
+
+def traffic_table():
+    p = ROOT / "profiles" / "traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text())
+        except ValueError:
+            return {}
+    return {}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    from spiral_amd import ops, synth, TYPE_Q4_0, TYPE_Q6_K, TYPE_Q8_0, lib
+    from spiral_amd import row_bytes
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a HIP device")
+    lib()  # fail loudly if the library is missing
+    dev = torch.device("cuda:0")
+    timer = Timer(torch)
+    steps, warmup = args.steps, args.warmup
+    results = {}
+
+    def upload_planar(qtype, n, k, seed, copies):
+        raw = synth.make_weights(qtype, n, k, seed)
+        src = torch.from_numpy(raw).to(dev)
+        first = ops.to_planar(qtype, src, n, k)
+        ws = [first] + [first.clone() for _ in range(copies - 1)]
+        del src
+        return raw, ws
+
+    def x_dev(m, k, seed):
+        x = synth.make_x(m, k, seed)
+        return x, torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(dev)
+
+    def record(name, wall, durs, per_launch, unit, peak, bound, extra=None):
+        mean = float(np.mean(durs))
+        achieved = per_launch / mean / (1e9 if unit == "GB/s" else 1e12)
+        whole = per_launch * steps / wall / (1e9 if unit == "GB/s" else 1e12)
+        r = {"value": whole, "unit": unit, "ms_per_step": wall / steps * 1e3,
+             "kernel_us_mean": mean * 1e6, "kernel_us_p10": float(np.percentile(durs, 10)) * 1e6,
+             "kernel_us_p90": float(np.percentile(durs, 90)) * 1e6,
+             "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                          "frac": achieved / peak}}
+        if extra:
+            r.update(extra)
+        results[name] = r
+
+    want = (lambda n: args.only in (None, n))
+
+    # --- Q8_0 GEMV (headline) -------------------------------------------------
+    if want("gemv_q8_0"):
+        n, k = 14336, 4096
+        wbytes = n * row_bytes(TYPE_Q8_0, k)
+        raw, ws = upload_planar(TYPE_Q8_0, n, k, 1, copies_for(wbytes))
+        x, xd = x_dev(1, k, 2)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q8_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q8_0", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q8_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
+                "bytes_per_launch": wbytes, "copies": len(ws)})
+        cpu_raw, cpu_x = raw, x
+        del ws
+
+    # --- Q6_K GEMV ------------------------------------------------------------
+    if want("gemv_q6_k"):
+        n, k = 4096, 14336
+        wbytes = n * row_bytes(TYPE_Q6_K, k)
+        _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies_for(wbytes))
+        _, xd = x_dev(1, k, 4)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q6_K, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q6_k", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q6_K decode GEMV y[4096] = W[4096x14336] x[14336], batch 1, bf16 out",
+                "bytes_per_launch": wbytes, "copies": len(ws)})
+        del ws
+
+    # --- Q4_0 GEMV ------------------------------------------------------------
+    if want("gemv_q4_0"):
+        n, k = 4096, 4096
+        wbytes = n * row_bytes(TYPE_Q4_0, k)
+        _, ws = upload_planar(TYPE_Q4_0, n, k, 5, copies_for(wbytes))
+        _, xd = x_dev(1, k, 6)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q4_0", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q4_0 decode GEMV y[4096] = W[4096x4096] x[4096], batch 1, bf16 out",
+                "bytes_per_launch": wbytes, "copies": len(ws)})
+        del ws
+
+    # --- Q4_0 -> bf16 dequant ---------------------------------------------------
+    if want("dequant_q4_0"):
+        n = k = 4096
+        inb = n * row_bytes(TYPE_Q4_0, k)
+        outb = n * k * 2
+        copies = copies_for(inb + outb)
+        _, ws = upload_planar(TYPE_Q4_0, n, k, 0, copies)
+        outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+        wall, durs = timer.run(lambda i: ops.dequant(TYPE_Q4_0, ws[i % copies], n, k, out=outs[i % copies]),
+                               steps, warmup)
+        record("dequant_q4_0", wall, durs, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q4_0 -> bf16 dequant, 4096x4096 (524,288 blocks)",
+                "bytes_per_launch": inb + outb, "packed_bytes": inb, "copies": copies})
+        results["dequant_q4_0"]["packed_GBps"] = inb / np.mean(durs) / 1e9
+        del ws, outs
+
+    # --- Q4_0 dequant-GEMM, M = 512 ---------------------------------------------
+    if want("gemm_q4_0"):
+        m, n, k = 512, 4096, 4096
+        wbytes = n * row_bytes(TYPE_Q4_0, k)
+        copies = copies_for(wbytes + m * k * 2 + m * n * 2)
+        _, ws = upload_planar(TYPE_Q4_0, n, k, 7, copies)
+        xs = [x_dev(m, k, 8 + c)[1] for c in range(copies)]
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        flops = 2.0 * m * n * k
+        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y),
+                               steps, warmup)
+        record("gemm_q4_0", wall, durs, flops, "TFLOP/s", MFMA_BF16_PEAK_TFS, "mfma",
+               {"workload": "Q4_0 prefill dequant-GEMM Y[512x4096] = X[512x4096] W[4096x4096]^T, bf16 MFMA, fp32 acc",
+                "flops_per_launch": flops, "copies": copies})
+        del ws, xs
+
+    # --- Q4_0 MoE grouped GEMM ----------------------------------------------------
+    if want("moe_q4_0"):
+        n_expert, hidden, inter2, inter = 128, 2048, 1536, 768
+        n_tokens, top_k = 64, 8
+        rng = np.random.default_rng(9)
+        ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+        touched = np.unique(ids).size
+        gu_per = inter2 * row_bytes(TYPE_Q4_0, hidden)
+        dn_per = hidden * row_bytes(TYPE_Q4_0, inter)
+        copies = max(2, int(np.ceil(2 * LLC_BYTES / (n_expert * (gu_per + dn_per)))))
+
+        def stacked(n, k, per, seed):
+            out = []
+            base_raw = synth.make_weights(TYPE_Q4_0, n, k, seed)
+            base = ops.to_planar(TYPE_Q4_0, torch.from_numpy(base_raw).to(dev), n, k)
+            for _ in range(copies):
+                w = torch.empty(n_expert * per, dtype=torch.uint8, device=dev)
+                # distinct experts: a per-expert byte rotation of one seeded matrix
+                for e in range(n_expert):
+                    w[e * per:(e + 1) * per] = torch.roll(base, e * 7)
+                out.append(w)
+            return out
+
+        gus = stacked(inter2, hidden, gu_per, 10)
+        dns = stacked(hidden, inter, dn_per, 11)
+        ids_d = torch.from_numpy(ids).to(dev)
+        _, x1 = x_dev(n_tokens, hidden, 12)
+        x1 = x1.view(n_tokens, 1, hidden)
+        _, x2 = x_dev(n_tokens * top_k, inter, 13)
+        x2 = x2.view(n_tokens, top_k, inter)
+        y1 = torch.empty((n_tokens, top_k, inter2), dtype=torch.bfloat16, device=dev)
+        y2 = torch.empty((n_tokens, top_k, hidden), dtype=torch.bfloat16, device=dev)
+        ws1 = ops.mul_mat_id_workspace(n_expert, n_tokens, top_k, dev)
+        ws2 = ops.mul_mat_id_workspace(n_expert, n_tokens, top_k, dev)
+
+        def launch(i):
+            c = i % copies
+            ops.mul_mat_id(TYPE_Q4_0, gus[c], gu_per, n_expert, inter2, hidden, x1, ids_d, workspace=ws1, out=y1)
+            ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, x2, ids_d, workspace=ws2, out=y2)
+
+        wall, durs = timer.run(launch, steps, warmup)
+        wbytes = touched * (gu_per + dn_per)
+        flops = 2.0 * n_tokens * top_k * (inter2 * hidden + hidden * inter)
+        record("moe_q4_0", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q4_0 MoE: 128 experts (gate_up 1536x2048, down 2048x768), 64 tokens, top-8; "
+                            "one step = gate_up + down MUL_MAT_ID",
+                "bytes_per_launch": wbytes, "touched_experts": int(touched),
+                "tflops": flops / float(np.mean(durs)) / 1e12, "copies": copies})
+        del gus, dns
+
+    if not results:
+        raise SystemExit(f"unknown workload {args.only}")
+
+    traffic = traffic_table()
+    head_name = "gemv_q8_0" if "gemv_q8_0" in results else next(iter(results))
+    head = results[head_name]
+    roof = dict(head["roofline"])
+    roof["traffic"] = traffic.get(head_name)
+
+    cpu = None
+    if head_name == "gemv_q8_0" and not args.no_cpu:
+        from oracle import oracle as O
+        threads = min(16, len(os.sched_getaffinity(0)))
+        n, k = 14336, 4096
+        O.quant_matmul_f32(O.Q8_0, cpu_raw, n, k, cpu_x, threads=threads)  # warm-up pass
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            O.quant_matmul_f32(O.Q8_0, cpu_raw, n, k, cpu_x, threads=threads)
+            passes += 1
+            if time.perf_counter() - t0 >= args.cpu_seconds:
+                break
+        dt = time.perf_counter() - t0
+        cpu = {"value": cpu_raw.size * passes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"{passes} full passes of the same Q8_0 14336x4096 GEMV (canonical GGUF bytes) "
+                         f"through the C oracle's streaming dequant+dot, OpenMP, {dt:.1f} s"}
+
+    line = {
+        "metric": "quant GEMV packed-weight GB/s (% of HBM peak); dequant-GEMM TFLOP/s (% MFMA)",
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": head.get("workload", head_name), "kernel": head_name},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "workloads": results,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

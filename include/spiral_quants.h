@@ -1,0 +1,181 @@
+/*
+ * spiral_quants.h -- C ABI of libspiral_quants.so, the MI355X (gfx950)
+ * implementation of spiral's quantized-weight hot path: GGUF Q4_0 / Q8_0 /
+ * Q6_K block dequantization to bf16 and the dequant-fused matrix products
+ * behind a ggml backend's MUL_MAT / GET_ROWS / MUL_MAT_ID.
+ *
+ * Conventions
+ *  - Plain C types only. Device pointers are HIP device memory; `stream` is a
+ *    hipStream_t passed as void* (NULL = the null stream). Every call is
+ *    asynchronous on that stream; nothing synchronizes unless stated.
+ *  - Return value: spiral_status (0 = SPIRAL_OK). Validation failures are
+ *    reported before anything is launched. No exceptions cross the ABI.
+ *  - Shapes use ggml's naming: a weight tensor has n_rows rows (ggml ne1,
+ *    the reference's weights_cols) of k elements (ggml ne0, the reference's
+ *    weights_rows). A product computes y[i][n] = sum_k x[i][k] * W[n][k].
+ *  - bf16 values travel as uint16_t bit patterns.
+ *  - Thread-safe for calls on distinct streams; the library keeps no mutable
+ *    global state.
+ */
+#ifndef SPIRAL_QUANTS_H
+#define SPIRAL_QUANTS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum spiral_status {
+  SPIRAL_OK = 0,
+  SPIRAL_ERR_SHAPE = 1,     /* k not a multiple of the block, size <= 0, bad ld */
+  SPIRAL_ERR_ALIGN = 2,     /* a device pointer is not 16-byte aligned */
+  SPIRAL_ERR_NULL = 3,      /* a required pointer is NULL */
+  SPIRAL_ERR_NO_DEVICE = 4, /* no HIP device is visible */
+  SPIRAL_ERR_HIP = 5,       /* a HIP runtime call or kernel launch failed */
+  SPIRAL_ERR_TYPE = 6,      /* unsupported tensor type or op */
+  SPIRAL_ERR_CAPACITY = 7,  /* a caller buffer is too small */
+  SPIRAL_ERR_RANGE = 8      /* an index is outside its tensor (host-checked) */
+} spiral_status;
+
+/* Tensor type ids: the values ggml uses for these types (ggml_type). */
+enum {
+  SPIRAL_TYPE_F32 = 0,
+  SPIRAL_TYPE_F16 = 1,
+  SPIRAL_TYPE_Q4_0 = 2,
+  SPIRAL_TYPE_Q8_0 = 8,
+  SPIRAL_TYPE_Q6_K = 14,
+  SPIRAL_TYPE_I32 = 26,
+  SPIRAL_TYPE_BF16 = 30
+};
+
+const char* spiral_status_string(int status);
+
+/* Number of visible HIP devices (0 when none); never fails. */
+int spiral_device_count(void);
+
+/* ===================================================================== *
+ * 1. The reference's host repack API, per format.                        *
+ *                                                                         *
+ * Same argument meaning, layout and 0-on-error convention as             *
+ * spiral::quants::<fmt>::record_count / packed_bytes / repack_weights     *
+ * (src/quants/q4_0/repack.h:10-111, src/quants/q8_0/repack.h:10-91,      *
+ * src/quants/q6_k/repack.h:11-115) and their C shim quants_record_count / *
+ * quants_packed_bytes / quants_repack (src/quants/tests/repack.cc:12-33), *
+ * which the reference builds once per format; here the format is part of  *
+ * the name. Host memory; the output is the reference's record stream,     *
+ * byte for byte. A subnormal fp16 scale is stored as +0 and one warning    *
+ * line goes to stderr per call (src/quants/common/repack.h:38-61).         *
+ * ===================================================================== */
+int64_t quants_q4_0_record_count(int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q4_0_packed_bytes(int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q4_0_repack(const uint8_t* src, int64_t src_col_stride_bytes,
+                           uint8_t* dst, int64_t dst_capacity,
+                           int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q8_0_record_count(int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q8_0_packed_bytes(int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q8_0_repack(const uint8_t* src, int64_t src_col_stride_bytes,
+                           uint8_t* dst, int64_t dst_capacity,
+                           int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q6_k_record_count(int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q6_k_packed_bytes(int64_t weights_rows, int64_t weights_cols);
+int64_t quants_q6_k_repack(const uint8_t* src, int64_t src_col_stride_bytes,
+                           uint8_t* dst, int64_t dst_capacity,
+                           int64_t weights_rows, int64_t weights_cols);
+
+/* ===================================================================== *
+ * 2. The reference's device entry points on the GPU, over its records.   *
+ * ===================================================================== */
+
+/* Replaces quants_unpack_all (src/quants/tests/unpack.aie.cc:21-45):
+ * exact bf16 dequantization of a reference record stream (from
+ * quants_<fmt>_repack, copied to the device) into the reference's output
+ * order [weights_cols/8][weights_rows/record_rows][chunk][rows][8]. Shapes are
+ * runtime arguments instead of -DQUANTS_WEIGHTS_ROWS/COLS. */
+int quants_unpack_all(int type, const void* packed, int64_t weights_rows,
+                      int64_t weights_cols, uint16_t* out, void* stream);
+
+/* Replaces quants_unpack_mmul_all (src/quants/tests/mmul.aie.cc:20-35):
+ * fused dequant + bf16 product with fp32 accumulation over a record stream.
+ * inputs: bf16 [weights_rows/8][4][8] (four input vectors, tiled by 8 along
+ * k); outputs: f32 [weights_cols/8][4][8], overwritten (the shim zeroes its
+ * outputs first). */
+int quants_unpack_mmul_all(int type, const void* packed,
+                           const uint16_t* inputs, float* outputs,
+                           int64_t weights_rows, int64_t weights_cols,
+                           void* stream);
+
+/* ===================================================================== *
+ * 3. The GPU weight layout and the ggml op surface.                      *
+ *                                                                         *
+ * A quantized weight lives on the device in "planar" layout: the fields of *
+ * the canonical GGUF blocks split into separate row-major planes, so every *
+ * 16-byte payload vector is 16-byte aligned. Same byte count as the         *
+ * canonical tensor; a pure permutation of its bytes.                        *
+ *   Q4_0: qs[n_rows][k/32][16]  | d[n_rows][k/32] (fp16)                     *
+ *   Q8_0: qs[n_rows][k/32][32]  | d[n_rows][k/32]                            *
+ *   Q6_K: ql[n_rows][k/256][128] | qh[..][64] | sc[..][16] | d[n_rows][k/256] *
+ * This is the GPU counterpart of the reference's load-time repack           *
+ * (src/quants/TODO.md:303-334). Weight pointers below are planar and must be *
+ * 16-byte aligned.                                                          *
+ * ===================================================================== */
+
+/* Canonical bytes per row / per tensor (also the planar size); 0 when k is
+ * not a multiple of the type's block or a size is not positive. */
+int64_t spiral_row_bytes(int type, int64_t k);
+int64_t spiral_tensor_bytes(int type, int64_t n_rows, int64_t k);
+
+/* Canonical GGUF rows (row n at src + n*src_row_stride) -> planar. */
+int spiral_to_planar(int type, const void* src, int64_t src_row_stride,
+                     int64_t n_rows, int64_t k, void* dst, void* stream);
+/* Planar -> canonical GGUF rows (inverse of spiral_to_planar). */
+int spiral_from_planar(int type, const void* src, int64_t n_rows, int64_t k,
+                       void* dst, int64_t dst_row_stride, void* stream);
+
+/* Exact dequantization, planar -> row-major bf16 out[n*ld_out + k]. Element
+ * values are bf16_rne(code * d) (Q4_0 code q-8, Q8_0 int8) and
+ * bf16_rne(d * sc * (q-32)) (Q6_K), d decoded as the reference's device does
+ * (exponent 0 -> +0; src/quants/common/scale.aie.h:9-27). Bit-identical to
+ * the reference's unpack (src/quants/<fmt>/unpack.aie.h). */
+int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k,
+                        uint16_t* out, int64_t ld_out, void* stream);
+
+/* ggml GET_ROWS with quantized src0: out[i] = dequant(W[ids[i]]), out_type
+ * BF16 or F32 (both carry the same exact bf16 value). ids are device int32;
+ * an id outside [0, n_rows) yields a row of zeros. */
+int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k,
+                    const int32_t* ids, int64_t n_ids, void* out, int out_type,
+                    int64_t ld_out, void* stream);
+
+/* ggml MUL_MAT with quantized src0: y[i][n] = sum_k x[i][k] * W[n][k] for
+ * i < m, x bf16 rows of stride ldx elements, y (BF16 or F32) rows of stride ldy
+ * elements. fp32 accumulation. m == 1 runs the streaming GEMV; larger m runs
+ * the MFMA dequant-GEMM. */
+int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k,
+                   const uint16_t* x, int64_t ldx, int64_t m, void* y,
+                   int y_type, int64_t ldy, void* stream);
+
+/* ggml MUL_MAT_ID with quantized, expert-stacked src0: for token t < n_tokens
+ * and slot s < top_k, y[t][s][:] = W[ids[t][s]] * x[t][s % x_slots][:].
+ *  w: n_expert planar matrices of [n_rows][k], expert e at w + e*expert_stride
+ *     (expert_stride >= spiral_tensor_bytes, multiple of 16).
+ *  x: bf16 [n_tokens][x_slots][k] with x_slots 1 (shared input) or top_k.
+ *  ids: device int32 [n_tokens][top_k]; an id outside [0, n_expert) gives a
+ *     zero output row.
+ *  y: [n_tokens][top_k][n_rows] of y_type (BF16 or F32).
+ *  workspace: device scratch of spiral_mul_mat_id_workspace_bytes() bytes
+ *     for the per-expert token lists (caller-owned, no allocation here). */
+int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens,
+                                          int64_t top_k);
+int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride,
+                      int64_t n_expert, int64_t n_rows, int64_t k,
+                      const uint16_t* x, int64_t x_slots, const int32_t* ids,
+                      int64_t n_tokens, int64_t top_k, void* y, int y_type,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPIRAL_QUANTS_H */

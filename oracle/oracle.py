@@ -1,0 +1,213 @@
+"""ctypes view of the CPU oracle -- TEST INFRASTRUCTURE ONLY.
+
+Loads oracle/liboracle.so (built by oracle/Makefile) and, when present, the
+reference's own repack shims compiled into oracle/_ref/. Only tests/,
+__graft_entry__.smoke() and bench.py's CPU-baseline leg import this module;
+the product library never does.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+Q4_0, Q8_0, Q6_K = 2, 8, 14
+BLOCK_ELEMS = {Q4_0: 32, Q8_0: 32, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q8_0: 34, Q6_K: 210}
+FORMAT_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q6_K: "q6_k"}
+
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        path = HERE / "liboracle.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        L = ctypes.CDLL(str(path))
+        L.oq_fp16_ieee.argtypes = [ctypes.c_uint16]
+        L.oq_fp16_ieee.restype = ctypes.c_float
+        L.oq_fp16_device.argtypes = [ctypes.c_uint16]
+        L.oq_fp16_device.restype = ctypes.c_float
+        L.oq_bf16_rne.argtypes = [ctypes.c_float]
+        L.oq_bf16_rne.restype = ctypes.c_uint16
+        L.oq_fp16_device_array.argtypes = [_p, _p, _i64]
+        L.oq_fp16_device_array.restype = None
+        L.oq_bf16_rne_array.argtypes = [_p, _p, _i64]
+        L.oq_bf16_rne_array.restype = None
+        L.oq_aie_q_times_d.argtypes = [ctypes.c_int, ctypes.c_uint16]
+        L.oq_aie_q_times_d.restype = ctypes.c_uint16
+        L.oq_aie_q6_k.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_uint16]
+        L.oq_aie_q6_k.restype = ctypes.c_uint16
+        L.oq_check_q_times_d.argtypes = [ctypes.POINTER(_i64)]
+        L.oq_check_q_times_d.restype = _i64
+        L.oq_check_q6_k.argtypes = [ctypes.c_int, ctypes.POINTER(_i64)]
+        L.oq_check_q6_k.restype = _i64
+        L.oq_check_split_identity.argtypes = []
+        L.oq_check_split_identity.restype = _i64
+        L.oq_dequant.argtypes = [ctypes.c_int, _p, _i64, _i64, _i64, _p, _i64]
+        L.oq_dequant.restype = ctypes.c_int
+        L.oq_get_rows.argtypes = [ctypes.c_int, _p, _i64, _i64, _i64, _p, _i64, _p, _i64]
+        L.oq_get_rows.restype = ctypes.c_int
+        L.oq_ref_record_count.argtypes = [ctypes.c_int, _i64, _i64]
+        L.oq_ref_record_count.restype = _i64
+        L.oq_ref_packed_bytes.argtypes = [ctypes.c_int, _i64, _i64]
+        L.oq_ref_packed_bytes.restype = _i64
+        L.oq_ref_repack.argtypes = [ctypes.c_int, _p, _i64, _p, _i64, _i64, _i64,
+                                    ctypes.POINTER(ctypes.c_int)]
+        L.oq_ref_repack.restype = _i64
+        L.oq_ref_unpack.argtypes = [ctypes.c_int, _p, _i64, _i64, _p]
+        L.oq_ref_unpack.restype = ctypes.c_int
+        L.oq_matmul_f64.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64]
+        L.oq_matmul_f64.restype = None
+        L.oq_matmul_f32.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64]
+        L.oq_matmul_f32.restype = None
+        L.oq_quant_matmul_f32.argtypes = [ctypes.c_int, _p, _i64, _i64, _i64, _p, _i64,
+                                          _i64, _p, _i64, ctypes.c_int]
+        L.oq_quant_matmul_f32.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def fp16_device(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oq_fp16_device_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def bf16_rne(f):
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, dtype=np.uint16)
+    lib().oq_bf16_rne_array(_ptr(f), _ptr(out), f.size)
+    return out
+
+
+def row_bytes(qtype, k):
+    return (k // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]
+
+
+def dequant(qtype, raw, n_rows, k, row_stride=None):
+    """Canonical rows -> uint16 bf16 bits, shape [n_rows, k]."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    row_stride = row_bytes(qtype, k) if row_stride is None else row_stride
+    out = np.empty((n_rows, k), dtype=np.uint16)
+    rc = lib().oq_dequant(qtype, _ptr(raw), row_stride, n_rows, k, _ptr(out), k)
+    if rc != 0:
+        raise ValueError("oracle dequant: bad shape")
+    return out
+
+
+def get_rows(qtype, raw, n_rows, k, ids):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    out = np.empty((ids.size, k), dtype=np.uint16)
+    rc = lib().oq_get_rows(qtype, _ptr(raw), row_bytes(qtype, k), n_rows, k,
+                           _ptr(ids), ids.size, _ptr(out), k)
+    if rc != 0:
+        raise ValueError("oracle get_rows: bad shape or id")
+    return out
+
+
+def ref_packed_bytes(qtype, weights_rows, weights_cols):
+    return lib().oq_ref_packed_bytes(qtype, weights_rows, weights_cols)
+
+
+def ref_repack(qtype, raw, weights_rows, weights_cols, stride=None):
+    """Canonical column-major bytes -> reference NPU records; (bytes, warnings)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    stride = row_bytes(qtype, weights_rows) if stride is None else stride
+    n = ref_packed_bytes(qtype, weights_rows, weights_cols)
+    dst = np.zeros(max(n, 1), dtype=np.uint8)
+    warn = ctypes.c_int(0)
+    written = lib().oq_ref_repack(qtype, _ptr(raw), stride, _ptr(dst), n,
+                                  weights_rows, weights_cols, ctypes.byref(warn))
+    if written != n or n == 0:
+        raise ValueError("oracle ref_repack failed")
+    return dst[:n], warn.value
+
+
+def ref_unpack(qtype, packed, weights_rows, weights_cols):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.empty(weights_rows * weights_cols, dtype=np.uint16)
+    rc = lib().oq_ref_unpack(qtype, _ptr(packed), weights_rows, weights_cols, _ptr(out))
+    if rc != 0:
+        raise ValueError("oracle ref_unpack: bad shape")
+    return out
+
+
+def ref_order(values_nk, record_rows):
+    """Row-major [N][K] -> the reference output order
+    [N/8][K/record_rows][record_rows][8] (formats/q4_0.py:65-79)."""
+    n, k = values_nk.shape
+    return (values_nk.T.reshape(k // record_rows, record_rows, n // 8, 8)
+            .transpose(2, 0, 1, 3).reshape(-1))
+
+
+REF_RECORD_ROWS = {Q4_0: 64, Q8_0: 256, Q6_K: 256}
+
+
+def matmul_f64(w_bf16, x_bf16):
+    """y[m, n] = sum_k x[m, k] * w[n, k] in float64 over bf16 bit arrays."""
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    n, k = w.shape
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    lib().oq_matmul_f64(_ptr(w), k, n, k, _ptr(x), k, m, _ptr(y), n)
+    return y
+
+
+def matmul_f32(w_bf16, x_bf16):
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    n, k = w.shape
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float32)
+    lib().oq_matmul_f32(_ptr(w), k, n, k, _ptr(x), k, m, _ptr(y), n)
+    return y
+
+
+def quant_matmul_f32(qtype, raw, n_rows, k, x_bf16, threads=1):
+    """Streaming dequantize-and-multiply on the CPU (the CPU baseline)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).reshape(-1, k)
+    m = x.shape[0]
+    y = np.empty((m, n_rows), dtype=np.float32)
+    rc = lib().oq_quant_matmul_f32(qtype, _ptr(raw), row_bytes(qtype, k), n_rows, k,
+                                   _ptr(x), k, m, _ptr(y), n_rows, threads)
+    if rc != 0:
+        raise ValueError("oracle quant_matmul: bad shape")
+    return y
+
+
+# ---- the reference's own repack, compiled from its sources into _ref/ ----
+
+def ref_shim(qtype):
+    """ctypes handle on oracle/_ref/libref_repack_<fmt>.so, or None."""
+    path = HERE / "_ref" / f"libref_repack_{FORMAT_NAMES[qtype]}.so"
+    if not path.exists():
+        return None
+    L = ctypes.CDLL(str(path))
+    L.quants_record_count.argtypes = [_i64, _i64]
+    L.quants_record_count.restype = _i64
+    L.quants_packed_bytes.argtypes = [_i64, _i64]
+    L.quants_packed_bytes.restype = _i64
+    L.quants_repack.argtypes = [_p, _i64, _p, _i64, _i64, _i64]
+    L.quants_repack.restype = _i64
+    return L
+
+
+def cpu_count():
+    return len(os.sched_getaffinity(0))

@@ -1,0 +1,23 @@
+"""spiral_amd: MI355X (gfx950) quantized-weight hot path of spiral.
+
+GGUF Q4_0 / Q8_0 / Q6_K exact dequantization to bf16 and the dequant-fused
+GEMV / GEMM / MoE grouped GEMM behind a ggml-style MUL_MAT / GET_ROWS /
+MUL_MAT_ID surface, as hand-written HIP kernels in libspiral_quants.so.
+
+    spiral_amd._lib     ctypes binding of the C ABI (include/spiral_quants.h)
+    spiral_amd.ops      device-tensor wrappers used by tests and bench.py
+    spiral_amd.quants   host mirror of the reference's repack harness
+    spiral_amd.synth    seeded synthetic GGUF tensors
+    spiral_amd.build    hipcc build of the library
+"""
+
+from ._lib import (TYPE_BF16, TYPE_F32, TYPE_I32, TYPE_Q4_0, TYPE_Q6_K, TYPE_Q8_0,  # noqa: F401
+                   SpiralError, lib)
+
+FORMATS = {"q4_0": TYPE_Q4_0, "q8_0": TYPE_Q8_0, "q6_k": TYPE_Q6_K}
+BLOCK_ELEMS = {TYPE_Q4_0: 32, TYPE_Q8_0: 32, TYPE_Q6_K: 256}
+BLOCK_BYTES = {TYPE_Q4_0: 18, TYPE_Q8_0: 34, TYPE_Q6_K: 210}
+
+
+def row_bytes(qtype, k):
+    return (k // BLOCK_ELEMS[qtype]) * BLOCK_BYTES[qtype]

@@ -1,0 +1,65 @@
+// Validation and dispatch for the matrix-product entry points.
+#include "common.h"
+
+namespace spiral {
+int64_t gemv_max_k(int type);
+int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
+         hipStream_t s);
+int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m,
+         void* y, int y_type, int64_t ldy, hipStream_t s);
+int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs);
+int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
+        const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
+        int y_type, void* workspace, hipStream_t s);
+}  // namespace spiral
+
+using namespace spiral;
+
+extern "C" {
+
+int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx,
+                   int64_t m, void* y, int y_type, int64_t ldy, void* stream) {
+  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
+  if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
+  if (w == nullptr || x == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
+  if (n_rows <= 0 || m <= 0 || k <= 0 || k % block_elems(type) != 0) return SPIRAL_ERR_SHAPE;
+  if (ldx < k || ldy < n_rows) return SPIRAL_ERR_SHAPE;
+  if (!aligned16(w) || !aligned16(x) || ldx % 8 != 0) return SPIRAL_ERR_ALIGN;
+  if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0) return SPIRAL_ERR_ALIGN;
+  int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (m == 1 && k <= gemv_max_k(type)) return gemv(type, w, n_rows, k, x, y, y_type, s);
+  return gemm(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
+}
+
+int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens, int64_t top_k) {
+  if (n_expert <= 0 || n_tokens < 0 || top_k <= 0) return 0;
+  return moe_workspace_bytes(n_expert, n_tokens * top_k);
+}
+
+int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,
+                      int64_t k, const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens,
+                      int64_t top_k, void* y, int y_type, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
+  if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
+  if (n_tokens == 0) return SPIRAL_OK;
+  if (w == nullptr || x == nullptr || ids == nullptr || y == nullptr || workspace == nullptr)
+    return SPIRAL_ERR_NULL;
+  if (n_expert <= 0 || n_rows <= 0 || k <= 0 || k % block_elems(type) != 0 || n_tokens < 0 || top_k <= 0)
+    return SPIRAL_ERR_SHAPE;
+  if (x_slots != 1 && x_slots != top_k) return SPIRAL_ERR_SHAPE;
+  if (expert_stride < spiral_tensor_bytes(type, n_rows, k) || expert_stride % 16 != 0) return SPIRAL_ERR_SHAPE;
+  if (n_tokens * top_k > INT32_MAX) return SPIRAL_ERR_SHAPE;
+  if (workspace_bytes < moe_workspace_bytes(n_expert, n_tokens * top_k)) return SPIRAL_ERR_CAPACITY;
+  if (!aligned16(w) || !aligned16(x) || k % 8 != 0) return SPIRAL_ERR_ALIGN;
+  if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0 || (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
+    return SPIRAL_ERR_ALIGN;
+  int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type,
+             workspace, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

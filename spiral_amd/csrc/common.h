@@ -1,0 +1,118 @@
+// Shared definitions for the gfx950 kernels: format constants, the planar
+// weight layout, scalar decode helpers and host-side validation.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "spiral_quants.h"
+
+namespace spiral {
+
+// ---- format constants -----------------------------------------------------
+// Canonical GGUF blocks (src/quants/q4_0/layout.h:11-16,
+// src/quants/q8_0/layout.h:11-14, src/quants/q6_k/layout.h:11-16).
+constexpr int kQ4_0Elems = 32, kQ4_0Bytes = 18;
+constexpr int kQ8_0Elems = 32, kQ8_0Bytes = 34;
+constexpr int kQ6_KElems = 256, kQ6_KBytes = 210;
+
+inline __host__ __device__ int block_elems(int type) {
+  return type == SPIRAL_TYPE_Q6_K ? kQ6_KElems
+         : (type == SPIRAL_TYPE_Q4_0 || type == SPIRAL_TYPE_Q8_0) ? 32
+                                                                   : 0;
+}
+inline __host__ __device__ int block_bytes(int type) {
+  return type == SPIRAL_TYPE_Q4_0   ? kQ4_0Bytes
+         : type == SPIRAL_TYPE_Q8_0 ? kQ8_0Bytes
+         : type == SPIRAL_TYPE_Q6_K ? kQ6_KBytes
+                                    : 0;
+}
+inline bool is_quant_type(int type) { return block_elems(type) != 0; }
+
+// ---- planar layout ----------------------------------------------------------
+// Plane base pointers of one planar matrix with n_rows rows of nb blocks.
+struct PlanarQ4_0 {
+  const uint8_t* qs;  // [n][nb][16]
+  const uint16_t* d;  // [n][nb]
+  __host__ __device__ PlanarQ4_0(const void* base, int64_t n_rows, int64_t nb)
+      : qs(static_cast<const uint8_t*>(base)),
+        d(reinterpret_cast<const uint16_t*>(qs + n_rows * nb * 16)) {}
+};
+struct PlanarQ8_0 {
+  const int8_t* qs;   // [n][nb][32]
+  const uint16_t* d;  // [n][nb]
+  __host__ __device__ PlanarQ8_0(const void* base, int64_t n_rows, int64_t nb)
+      : qs(static_cast<const int8_t*>(base)),
+        d(reinterpret_cast<const uint16_t*>(static_cast<const uint8_t*>(base) +
+                                            n_rows * nb * 32)) {}
+};
+struct PlanarQ6_K {
+  const uint8_t* ql;  // [n][nb][128]
+  const uint8_t* qh;  // [n][nb][64]
+  const int8_t* sc;   // [n][nb][16]
+  const uint16_t* d;  // [n][nb]
+  __host__ __device__ PlanarQ6_K(const void* base, int64_t n_rows, int64_t nb)
+      : ql(static_cast<const uint8_t*>(base)),
+        qh(ql + n_rows * nb * 128),
+        sc(reinterpret_cast<const int8_t*>(ql + n_rows * nb * 192)),
+        d(reinterpret_cast<const uint16_t*>(ql + n_rows * nb * 208)) {}
+};
+
+// ---- scalar decode ------------------------------------------------------------
+
+// Block-scale decode with the reference's device rule
+// (src/quants/common/scale.aie.h:14-27): exponent 0 (zero or subnormal) gives
+// +0, exponent 31 gives the finite 2^16 * (1.m), otherwise IEEE binary16.
+__device__ __forceinline__ float fp16_scale(uint32_t h) {
+  const uint32_t e = (h >> 10) & 31u;
+  const uint32_t bits =
+      ((h & 0x8000u) << 16) | ((e + 112u) << 23) | ((h & 0x3ffu) << 13);
+  return e ? __uint_as_float(bits) : 0.0f;
+}
+
+// Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even.
+// Lowers to v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+  bf16x2_t v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load for payload read exactly once per kernel; the
+// non-temporal hint keeps it from displacing reused data (x, scales) in cache.
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---- host-side helpers ----------------------------------------------------------
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? SPIRAL_OK : SPIRAL_ERR_HIP;
+}
+
+// Checks that a device is visible; the first failing call is reported as
+// SPIRAL_ERR_NO_DEVICE so callers can tell "no GPU" from a kernel failure.
+int require_device();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Compute units of the current device (cached per device id).
+int device_cu_count();
+
+}  // namespace spiral

@@ -1,0 +1,127 @@
+// Exact dequantization of planar Q4_0 / Q8_0 / Q6_K weights to bf16, and the
+// GET_ROWS gather built on it.
+//
+// Element values follow the reference's unpack semantics exactly:
+//   Q4_0  bf16_rne((q - 8) * d)        src/quants/q4_0/unpack.aie.h:31-46
+//   Q8_0  bf16_rne(q * d)              src/quants/q8_0/unpack.aie.h:37-52
+//   Q6_K  bf16_rne(d * sc * (q - 32))  src/quants/q6_k/unpack.aie.h:33-138
+// The reference reaches these values through split bf16 scale terms; every
+// product here is exact in fp32 (<= 23 significant bits) so one rounding
+// (v_cvt_pk_bf16_f32, round-to-nearest-even) gives the same bits.
+//
+// Work item: one group of 8 consecutive output elements of one row, written
+// as one 16-byte store, so consecutive lanes store consecutive 16 bytes.
+#include "common.h"
+#include "dequant_impl.h"
+
+namespace spiral {
+namespace {
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
+                                                      int64_t nb, int64_t groups_per_row,
+                                                      uint16_t* __restrict__ out, int64_t ld_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_rows * groups_per_row) return;
+  const int64_t n = i / groups_per_row, g = i % groups_per_row;
+  float v[8];
+  dequant8<TYPE>(w, n_rows, nb, n, g, v);
+  uint4 o;
+  o.x = pack_bf16x2(v[0], v[1]);
+  o.y = pack_bf16x2(v[2], v[3]);
+  o.z = pack_bf16x2(v[4], v[5]);
+  o.w = pack_bf16x2(v[6], v[7]);
+  *reinterpret_cast<uint4*>(out + n * ld_out + 8 * g) = o;
+}
+
+template <int TYPE, bool F32_OUT>
+__global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
+                                                       int64_t nb, int64_t groups_per_row,
+                                                       const int32_t* __restrict__ ids, int64_t n_ids,
+                                                       void* __restrict__ out, int64_t ld_out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_ids * groups_per_row) return;
+  const int64_t r = i / groups_per_row, g = i % groups_per_row;
+  const int64_t n = ids[r];
+  float v[8];
+  if (n >= 0 && n < n_rows) {
+    dequant8<TYPE>(w, n_rows, nb, n, g, v);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+  }
+  uint4 o;
+  o.x = pack_bf16x2(v[0], v[1]);
+  o.y = pack_bf16x2(v[2], v[3]);
+  o.z = pack_bf16x2(v[4], v[5]);
+  o.w = pack_bf16x2(v[6], v[7]);
+  if constexpr (F32_OUT) {
+    // The F32 output carries the same exact bf16 values, widened.
+    float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + r * ld_out + 8 * g);
+    p[0] = make_float4(bf16_lo(o.x), bf16_hi(o.x), bf16_lo(o.y), bf16_hi(o.y));
+    p[1] = make_float4(bf16_lo(o.z), bf16_hi(o.z), bf16_lo(o.w), bf16_hi(o.w));
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + r * ld_out + 8 * g) = o;
+  }
+}
+
+}  // namespace
+}  // namespace spiral
+
+using namespace spiral;
+
+extern "C" {
+
+int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k, uint16_t* out,
+                        int64_t ld_out, void* stream) {
+  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
+  if (w == nullptr || out == nullptr) return SPIRAL_ERR_NULL;
+  if (n_rows <= 0 || k <= 0 || k % block_elems(type) != 0 || ld_out < k) return SPIRAL_ERR_SHAPE;
+  if (!aligned16(w) || !aligned16(out) || ld_out % 8 != 0) return SPIRAL_ERR_ALIGN;
+  int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  const int64_t nb = k / block_elems(type), gpr = k / 8;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_rows * gpr, 256)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* W = static_cast<const uint8_t*>(w);
+  if (type == SPIRAL_TYPE_Q4_0)
+    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q4_0>, grid, dim3(256), 0, s, W, n_rows, nb, gpr, out, ld_out);
+  else if (type == SPIRAL_TYPE_Q8_0)
+    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q8_0>, grid, dim3(256), 0, s, W, n_rows, nb, gpr, out, ld_out);
+  else
+    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q6_K>, grid, dim3(256), 0, s, W, n_rows, nb, gpr, out, ld_out);
+  return launch_status();
+}
+
+int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k, const int32_t* ids,
+                    int64_t n_ids, void* out, int out_type, int64_t ld_out, void* stream) {
+  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
+  if (out_type != SPIRAL_TYPE_BF16 && out_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
+  if (n_ids == 0) return SPIRAL_OK;
+  if (w == nullptr || out == nullptr || ids == nullptr) return SPIRAL_ERR_NULL;
+  if (n_rows <= 0 || n_ids < 0 || k <= 0 || k % block_elems(type) != 0 || ld_out < k)
+    return SPIRAL_ERR_SHAPE;
+  if (!aligned16(w) || !aligned16(out) || ld_out % 8 != 0) return SPIRAL_ERR_ALIGN;
+  int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  const int64_t nb = k / block_elems(type), gpr = k / 8;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_ids * gpr, 256)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint8_t* W = static_cast<const uint8_t*>(w);
+#define SPIRAL_GET_ROWS(T)                                                                      \
+  do {                                                                                          \
+    if (out_type == SPIRAL_TYPE_F32)                                                            \
+      hipLaunchKernelGGL((get_rows_kernel<T, true>), grid, dim3(256), 0, s, W, n_rows, nb, gpr, \
+                         ids, n_ids, out, ld_out);                                              \
+    else                                                                                        \
+      hipLaunchKernelGGL((get_rows_kernel<T, false>), grid, dim3(256), 0, s, W, n_rows, nb,     \
+                         gpr, ids, n_ids, out, ld_out);                                         \
+  } while (0)
+  if (type == SPIRAL_TYPE_Q4_0) SPIRAL_GET_ROWS(SPIRAL_TYPE_Q4_0);
+  else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_GET_ROWS(SPIRAL_TYPE_Q8_0);
+  else SPIRAL_GET_ROWS(SPIRAL_TYPE_Q6_K);
+#undef SPIRAL_GET_ROWS
+  return launch_status();
+}
+
+}  // extern "C"

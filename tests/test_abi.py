@@ -1,0 +1,138 @@
+"""CPU tests of libspiral_quants.so's C ABI (no GPU needed).
+
+- every function declared in include/*.h is exported;
+- the reference-layout host repack (quants_<fmt>_*) is byte-identical to the
+  reference's own repack (oracle/_ref when built here, committed fixtures
+  everywhere) with the same 0-on-error convention and warning lines;
+- argument validation returns its status codes before any device work.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from spiral_amd import _lib, quants
+
+ROOT = Path(__file__).resolve().parent.parent
+GOLDEN = ROOT / "tests" / "golden"
+NAMES = {O.Q4_0: "q4_0", O.Q8_0: "q8_0", O.Q6_K: "q6_k"}
+
+
+def declared_functions():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"\b([A-Za-z_]\w*)\s*\(", text):
+            name = m.group(1)
+            if name.startswith(("spiral_", "quants_")):
+                names.add(name)
+    return sorted(names)
+
+
+def test_every_declared_symbol_is_exported(spiral_lib):
+    names = declared_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(spiral_lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_signatures_cover_the_header():
+    assert set(declared_functions()) <= set(_lib.SIGNATURES) | {
+        n for n in declared_functions() if n.startswith("spiral_backend") or n.startswith("spiral_buffer")
+        or n.startswith("spiral_graph") or n.startswith("spiral_tensor_")}
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+def test_host_repack_matches_reference_fixture(spiral_lib, qtype):
+    fx = np.load(GOLDEN / "ref_records.npz")
+    name = NAMES[qtype]
+    raw = fx[f"{name}_raw"]
+    rows, cols = (int(v) for v in fx[f"{name}_shape"])
+    got = quants.repack_host(name, raw, rows, cols, O.row_bytes(qtype, rows))
+    assert np.array_equal(got, fx[f"{name}_records"])
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+def test_host_repack_matches_reference_build(spiral_lib, qtype, capfd):
+    shim = O.ref_shim(qtype)
+    if shim is None:
+        pytest.skip("reference repack not built here (oracle/_ref)")
+    name = NAMES[qtype]
+    rng = np.random.default_rng(77 + qtype)
+    rows, cols = 768, 40
+    stride = O.row_bytes(qtype, rows) + 10  # padded column view
+    raw = rng.integers(0, 256, cols * stride, dtype=np.uint8)
+    blocks_view = raw.reshape(cols, stride)[:, :O.row_bytes(qtype, rows)].reshape(cols, -1, O.BLOCK_BYTES[qtype])
+    dpos = 208 if qtype == O.Q6_K else 0
+    blocks_view[:, ::3, dpos + 1] &= 0x83
+    want = np.zeros(shim.quants_packed_bytes(rows, cols), dtype=np.uint8)
+    assert shim.quants_repack(raw.ctypes.data, stride, want.ctypes.data, want.size, rows, cols) == want.size
+    ref_err = capfd.readouterr().err
+    got = quants.repack_host(name, raw, rows, cols, stride)
+    ours_err = capfd.readouterr().err
+    assert np.array_equal(got, want)
+    assert ours_err == ref_err and ours_err.count("\n") == 1
+
+
+@pytest.mark.parametrize("name", ["q4_0", "q8_0", "q6_k"])
+def test_host_repack_errors_return_zero(spiral_lib, name):
+    L = spiral_lib
+    rc = getattr(L, f"quants_{name}_record_count")
+    pb = getattr(L, f"quants_{name}_packed_bytes")
+    rp = getattr(L, f"quants_{name}_repack")
+    record_rows = quants.CONSTANTS[name]["kRecordRows"]
+    assert rc(record_rows, 8) == 1 and rc(record_rows, 7) == 0 and rc(record_rows - 32, 8) == 0
+    assert rc(0, 8) == 0 and rc(record_rows, 0) == 0 and rc(-record_rows, 8) == 0
+    assert pb(record_rows * 2, 16) == 4 * quants.CONSTANTS[name]["kPackedRecordBytes"]
+    qtype = {"q4_0": O.Q4_0, "q8_0": O.Q8_0, "q6_k": O.Q6_K}[name]
+    stride = O.row_bytes(qtype, record_rows)
+    src = np.zeros(8 * stride, dtype=np.uint8)
+    dst = np.zeros(pb(record_rows, 8), dtype=np.uint8)
+    vp = ctypes.c_void_p
+    assert rp(vp(src.ctypes.data), stride, vp(dst.ctypes.data), dst.size, record_rows, 8) == dst.size
+    assert rp(vp(src.ctypes.data), stride, vp(dst.ctypes.data), dst.size - 1, record_rows, 8) == 0
+    assert rp(vp(src.ctypes.data), stride - 1, vp(dst.ctypes.data), dst.size, record_rows, 8) == 0
+    assert rp(None, stride, vp(dst.ctypes.data), dst.size, record_rows, 8) == 0
+    assert rp(vp(src.ctypes.data), stride, None, dst.size, record_rows, 8) == 0
+
+
+def test_sizes(spiral_lib):
+    L = spiral_lib
+    assert L.spiral_row_bytes(_lib.TYPE_Q4_0, 4096) == 2304
+    assert L.spiral_row_bytes(_lib.TYPE_Q8_0, 4096) == 4352
+    assert L.spiral_row_bytes(_lib.TYPE_Q6_K, 14336) == 11760
+    assert L.spiral_row_bytes(_lib.TYPE_Q6_K, 100) == 0
+    assert L.spiral_row_bytes(_lib.TYPE_F32, 64) == 0
+    assert L.spiral_tensor_bytes(_lib.TYPE_Q8_0, 14336, 4096) == 62_390_272
+    assert L.spiral_tensor_bytes(_lib.TYPE_Q6_K, 4096, 14336) == 48_168_960
+    assert L.spiral_tensor_bytes(_lib.TYPE_Q4_0, 4096, 4096) == 9_437_184
+    assert L.spiral_mul_mat_id_workspace_bytes(128, 64, 8) == 4 * (129 + 512)
+
+
+def test_validation_before_device_work(spiral_lib):
+    """Bad arguments are reported without touching a device; with valid
+    arguments and no device the call says so (SPIRAL_ERR_NO_DEVICE) instead
+    of falling back to anything."""
+    L = spiral_lib
+    p = ctypes.c_void_p(4096)  # aligned dummy pointer, never dereferenced
+    q4 = _lib.TYPE_Q4_0
+    assert L.spiral_dequant_bf16(_lib.TYPE_F32, p, 4, 64, p, 64, None) == 6
+    assert L.spiral_dequant_bf16(q4, None, 4, 64, p, 64, None) == 3
+    assert L.spiral_dequant_bf16(q4, p, 4, 48, p, 64, None) == 1
+    assert L.spiral_dequant_bf16(q4, p, 0, 64, p, 64, None) == 1
+    assert L.spiral_dequant_bf16(q4, ctypes.c_void_p(4100), 4, 64, p, 64, None) == 2
+    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 1, p, _lib.TYPE_I32, 4, None) == 6
+    assert L.spiral_mul_mat(q4, p, 4, 64, p, 60, 1, p, _lib.TYPE_F32, 4, None) == 1
+    assert L.spiral_mul_mat(_lib.TYPE_Q6_K, p, 4, 64, p, 64, 1, p, _lib.TYPE_F32, 4, None) == 1
+    assert L.spiral_get_rows(q4, p, 4, 64, p, 0, p, _lib.TYPE_F32, 64, None) == 0  # empty is a no-op
+    assert L.spiral_mul_mat_id(q4, p, 32, 4, 4, 64, p, 3, p, 2, 2, p, _lib.TYPE_F32, p, 1 << 20, None) == 1
+    assert L.spiral_mul_mat_id(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, p, _lib.TYPE_F32, p, 4, None) == 7
+    assert L.quants_unpack_all(q4, p, 96, 8, p, None) == 1
+    if L.spiral_device_count() == 0:
+        assert L.spiral_dequant_bf16(q4, p, 4, 64, p, 64, None) == 4
+        assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 1, p, _lib.TYPE_F32, 4, None) == 4
+        assert L.quants_unpack_all(q4, p, 64, 8, p, None) == 4

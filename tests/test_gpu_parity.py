@@ -1,0 +1,276 @@
+"""GPU parity: libspiral_quants.so against the CPU oracle, through the C ABI.
+
+Bars:
+  - layout conversion, dequant, GET_ROWS, reference-record unpack: bit-exact
+    (uint16 bf16 patterns compared with array_equal, zero signs included);
+  - products: max |y - y_ref| / max(|y_ref|, rms(y_ref)) <= 1e-2 against a
+    float64 oracle over the exact bf16 weights (REL_TOL); the dense and MoE
+    GEMMs use bf16 weights like the reference and are also held to 1e-3 with
+    float32 output (REL_TOL_EXACT_W).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from spiral_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+REL_TOL_EXACT_W = 1e-3
+FORMATS = [O.Q4_0, O.Q8_0, O.Q6_K]
+NAMES = {O.Q4_0: "q4_0", O.Q8_0: "q8_0", O.Q6_K: "q6_k"}
+
+
+def bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def dev_u8(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).to(device)
+
+
+def dev_bf16(a_u16, device):
+    return torch.from_numpy(np.ascontiguousarray(a_u16, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    rms = np.sqrt(np.mean(ref * ref))
+    return float(np.max(np.abs(y - ref) / np.maximum(np.abs(ref), rms)))
+
+
+def weights_with_specials(qtype, n_rows, k, seed):
+    raw = synth.make_weights(qtype, n_rows, k, seed)
+    blocks = raw.reshape(-1, O.BLOCK_BYTES[qtype])
+    dpos = 208 if qtype == O.Q6_K else 0
+    rng = np.random.default_rng(seed + 1)
+    pick = rng.integers(0, blocks.shape[0], 16)
+    specials = np.array([0x0000, 0x8000, 0x0001, 0x83FF, 0x7C00, 0xFC01, 0x7BFF, 0x0400] * 2, dtype=np.uint16)
+    blocks[pick, dpos] = specials & 0xFF
+    blocks[pick, dpos + 1] = specials >> 8
+    if qtype == O.Q6_K:  # full int8 range of sub-scales on a few blocks
+        blocks[pick[:4], 192:208] = rng.integers(0, 256, (4, 16), dtype=np.uint8)
+    return raw
+
+
+# ---- layout and dequant --------------------------------------------------------
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_planar_round_trip(cuda, qtype):
+    n, k = 37, O.BLOCK_ELEMS[qtype] * 6
+    raw = synth.make_weights(qtype, n, k, 1)
+    rb = O.row_bytes(qtype, k)
+    for pad in (0, 14):
+        src = np.zeros((n, rb + pad), dtype=np.uint8)
+        src[:, :rb] = raw.reshape(n, rb)
+        planar = ops.to_planar(qtype, dev_u8(src, cuda), n, k, row_stride=rb + pad)
+        back = ops.from_planar(qtype, planar, n, k, row_stride=rb + pad)
+        torch.cuda.synchronize()
+        assert planar.numel() == raw.size  # byte-count preserving
+        assert np.array_equal(back.cpu().numpy().reshape(n, rb + pad)[:, :rb], raw.reshape(n, rb))
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_dequant_bit_exact_with_special_scales(cuda, qtype):
+    n, k = 64, O.BLOCK_ELEMS[qtype] * 8
+    raw = weights_with_specials(qtype, n, k, 5)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    got = bits(ops.dequant(qtype, w, n, k))
+    assert np.array_equal(got, O.dequant(qtype, raw, n, k))
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_dequant_golden_blocks(cuda, qtype):
+    import json
+    from pathlib import Path
+    cases = json.loads((Path(__file__).parent / "golden" / "special_blocks.json").read_text())
+    cases = [c for c in cases if c["format"] == NAMES[qtype]]
+    raw = np.concatenate([np.array(c["block"], dtype=np.uint8) for c in cases])
+    k = O.BLOCK_ELEMS[qtype]
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), len(cases), k)
+    got = bits(ops.dequant(qtype, w, len(cases), k))
+    for i, c in enumerate(cases):
+        assert got[i].tolist() == c["bf16"], c["name"]
+
+
+def test_dequant_q4_0_4096x4096_bit_exact(cuda):
+    """The Q4_0 -> bf16 workload at full size: 524,288 blocks."""
+    n = k = 4096
+    raw = synth.make_weights(O.Q4_0, n, k, 0)
+    w = ops.to_planar(O.Q4_0, dev_u8(raw, cuda), n, k)
+    got = bits(ops.dequant(O.Q4_0, w, n, k))
+    assert np.array_equal(got, O.dequant(O.Q4_0, raw, n, k))
+
+
+def test_dequant_q6_k_4096x14336_bit_exact(cuda):
+    n, k = 4096, 14336
+    raw = synth.make_weights(O.Q6_K, n, k, 2)
+    w = ops.to_planar(O.Q6_K, dev_u8(raw, cuda), n, k)
+    got = bits(ops.dequant(O.Q6_K, w, n, k))
+    assert np.array_equal(got, O.dequant(O.Q6_K, raw, n, k))
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_get_rows(cuda, qtype):
+    n, k = 50, O.BLOCK_ELEMS[qtype] * 4
+    raw = weights_with_specials(qtype, n, k, 9)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    ids = np.array([0, 49, 7, 7, 23, 1], dtype=np.int32)
+    want = O.get_rows(qtype, raw, n, k, ids)
+    ids_t = torch.from_numpy(ids).to(cuda)
+    got16 = bits(ops.get_rows(qtype, w, n, k, ids_t, out_dtype=torch.bfloat16))
+    got32 = ops.get_rows(qtype, w, n, k, ids_t, out_dtype=torch.float32).cpu().numpy()
+    assert np.array_equal(got16, want)
+    assert np.array_equal(got32.view(np.uint32), want.astype(np.uint32) << 16)
+    bad = torch.tensor([3, -1, 50], dtype=torch.int32, device=cuda)
+    z = ops.get_rows(qtype, w, n, k, bad, out_dtype=torch.float32).cpu().numpy()
+    row3 = O.get_rows(qtype, raw, n, k, np.array([3], np.int32))[0]
+    assert np.array_equal(z[0].view(np.uint32), row3.astype(np.uint32) << 16)
+    assert not z[1:].any()
+
+
+# ---- products -----------------------------------------------------------------
+
+def _mul_mat_case(cuda, qtype, n, k, m, seed, out_dtype):
+    raw = synth.make_weights(qtype, n, k, seed)
+    x = synth.make_x(m, k, seed + 100)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    y = ops.mul_mat(qtype, w, n, k, dev_bf16(x, cuda), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    ref = O.matmul_f64(O.dequant(qtype, raw, n, k), x)
+    return y.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gemv_small(cuda, qtype, out_dtype):
+    k = O.BLOCK_ELEMS[qtype] * 12
+    for n in (1, 7, 129):
+        y, ref = _mul_mat_case(cuda, qtype, n, k, 1, 20 + n, out_dtype)
+        assert rel_err(y, ref) <= REL_TOL, (n, rel_err(y, ref))
+
+
+@pytest.mark.parametrize("qtype,n,k", [(O.Q8_0, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q4_0, 4096, 4096)])
+def test_gemv_workload_shapes(cuda, qtype, n, k):
+    y, ref = _mul_mat_case(cuda, qtype, n, k, 1, 3, torch.bfloat16)
+    err = rel_err(y, ref)
+    print(f"gemv {NAMES[qtype]} {n}x{k}: rel err {err:.2e}")
+    assert err <= REL_TOL
+
+
+def test_gemv_catches_a_planted_oracle_error(cuda):
+    """The tolerance is tight enough to see a single wrong block scale."""
+    qtype, n, k = O.Q8_0, 64, 4096
+    raw = synth.make_weights(qtype, n, k, 8)
+    x = synth.make_x(1, k, 9)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    y = ops.mul_mat(qtype, w, n, k, dev_bf16(x, cuda), out_dtype=torch.float32).cpu().numpy()
+    bad = raw.copy().reshape(-1, 34)
+    bad[5, 1] ^= 0x04  # one block's fp16 d off by a power of two
+    ref = O.matmul_f64(O.dequant(qtype, bad.reshape(-1), n, k), x)
+    assert rel_err(y, ref) > REL_TOL
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("m,n,k_blocks", [(2, 64, 8), (100, 200, 12), (130, 257, 9)])
+def test_gemm_ragged(cuda, qtype, m, n, k_blocks):
+    k = O.BLOCK_ELEMS[qtype] * k_blocks
+    y, ref = _mul_mat_case(cuda, qtype, n, k, m, 30 + m, torch.float32)
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W, rel_err(y, ref)
+
+
+def test_gemm_q4_0_prefill_512x4096x4096(cuda):
+    y, ref = _mul_mat_case(cuda, O.Q4_0, 4096, 4096, 512, 4, torch.bfloat16)
+    err = rel_err(y, ref)
+    print(f"gemm q4_0 512x4096x4096: rel err {err:.2e}")
+    assert err <= REL_TOL
+
+
+# ---- MoE grouped GEMM -----------------------------------------------------------
+
+def _moe_case(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, out_dtype):
+    rng = np.random.default_rng(seed)
+    per = O.row_bytes(qtype, k) * n
+    raws = [synth.make_weights(qtype, n, k, seed * 1000 + e) for e in range(n_expert)]
+    w = torch.empty(n_expert * per, dtype=torch.uint8, device=cuda)
+    for e, r in enumerate(raws):
+        w[e * per:(e + 1) * per] = ops.to_planar(qtype, dev_u8(r, cuda), n, k)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    x = synth.make_x(n_tokens * x_slots, k, seed + 7).reshape(n_tokens, x_slots, k)
+    y = ops.mul_mat_id(qtype, w, per, n_expert, n, k, dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda),
+                       out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    y = y.float().cpu().numpy()
+    deq = {}
+    ref = np.zeros((n_tokens, top_k, n))
+    for t in range(n_tokens):
+        for s in range(top_k):
+            e = ids[t, s]
+            if e not in deq:
+                deq[e] = O.dequant(qtype, raws[e], n, k)
+            ref[t, s] = O.matmul_f64(deq[e], x[t, s % x_slots][None, :])[0]
+    return y, ref, ids
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_moe_small(cuda, qtype):
+    k = O.BLOCK_ELEMS[qtype] * 4
+    y, ref, _ = _moe_case(cuda, qtype, 8, 96, k, 40, 3, 1, 11, torch.float32)
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W
+
+
+def test_moe_per_slot_inputs_and_bad_ids(cuda):
+    qtype, n_expert, n, k = O.Q4_0, 6, 64, 256
+    y, ref, ids = _moe_case(cuda, qtype, n_expert, n, k, 70, 2, 2, 12, torch.float32)
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W  # 70 tokens over 6 experts: > 64 per expert
+    per = O.row_bytes(qtype, k) * n
+    w = torch.zeros(n_expert * per, dtype=torch.uint8, device=cuda)
+    bad = torch.tensor([[0, 9], [-3, 1]], dtype=torch.int32, device=cuda)
+    x = torch.zeros((2, 1, k), dtype=torch.bfloat16, device=cuda)
+    out = torch.full((2, 2, n), 7.0, device=cuda)
+    ops.mul_mat_id(qtype, w, per, n_expert, n, k, x, bad, out=out)
+    assert not out.cpu().numpy().any()
+
+
+def test_moe_128_experts_gate_up(cuda):
+    """The MoE workload's gate_up stage: 128 experts of 1536 x 2048 Q4_0,
+    64 tokens, top-8 distinct experts per token."""
+    y, ref, _ = _moe_case(cuda, O.Q4_0, 128, 1536, 2048, 64, 8, 1, 13, torch.bfloat16)
+    err = rel_err(y, ref)
+    print(f"moe gate_up: rel err {err:.2e}")
+    assert err <= REL_TOL
+
+
+# ---- the reference's device entry points over its records ------------------------
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_ref_unpack_all_bit_exact(cuda, qtype):
+    from pathlib import Path
+    fx = np.load(Path(__file__).parent / "golden" / "ref_records.npz")
+    name = NAMES[qtype]
+    raw, rec = fx[f"{name}_raw"], fx[f"{name}_records"]
+    rows, cols = (int(v) for v in fx[f"{name}_shape"])
+    got = bits(ops.unpack_all(qtype, dev_u8(rec, cuda), rows, cols))
+    assert np.array_equal(got, O.ref_unpack(qtype, rec, rows, cols))
+    assert np.array_equal(got, O.ref_order(O.dequant(qtype, raw, cols, rows), O.REF_RECORD_ROWS[qtype]))
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_ref_unpack_mmul_all(cuda, qtype):
+    rows, cols = 512, 48
+    raw = synth.make_weights(qtype, cols, rows, 40)
+    from spiral_amd import quants
+    rec = quants.repack_host(NAMES[qtype], raw, rows, cols, O.row_bytes(qtype, rows))
+    rng = np.random.default_rng(41)
+    inputs_rows = rng.integers(-4, 5, (4, rows)).astype(np.float32)  # src/quants/tests/mmul.py:22-35
+    tiled = inputs_rows.reshape(4, rows // 8, 8).transpose(1, 0, 2).reshape(-1)
+    x = synth.bf16_bits(tiled)
+    out = ops.unpack_mmul_all(qtype, dev_u8(rec, cuda), dev_bf16(x, cuda), rows, cols).cpu().numpy()
+    w = O.dequant(qtype, raw, cols, rows)
+    ref = O.matmul_f64(w, synth.bf16_bits(inputs_rows))  # [4, cols]
+    ref_tiled = ref.reshape(4, cols // 8, 8).transpose(1, 0, 2).reshape(-1)
+    assert rel_err(out, ref_tiled) <= REL_TOL_EXACT_W

@@ -1,0 +1,289 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each oracle function is checked by something other than its own formula:
+  - fp16 decode: numpy's IEEE binary16 for normal exponents, the reference's
+    documented special cases (src/quants/common/scale.aie.h:14-27) for the rest;
+  - bf16 rounding: torch's float32 -> bfloat16 conversion;
+  - dequant closed form: the reference's split-scale device arithmetic, step by
+    step, exhaustively (oq_check_*); exact rational arithmetic on random blocks;
+    hand-computed golden blocks (tests/golden/special_blocks.json);
+  - record layout: the reference's own repack.h compiled into oracle/_ref, and
+    fixtures made from it (tests/golden/ref_records.npz);
+  - matmul: numpy float64.
+"""
+
+import ctypes
+import json
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+FORMATS = [O.Q4_0, O.Q8_0, O.Q6_K]
+
+
+# ---- scalar conversions ---------------------------------------------------
+
+def _fp16_expected(h):
+    """Device decode rule from the reference text, via numpy for normals."""
+    h = np.asarray(h, dtype=np.uint16)
+    e = (h >> 10) & 31
+    out = h.view(np.float16).astype(np.float32)
+    out = np.where(e == 0, np.float32(0.0), out)
+    m = (h & 0x3FF).astype(np.float64)
+    sign = np.where(h & 0x8000, -1.0, 1.0)
+    big = (sign * 65536.0 * (1.0 + m / 1024.0)).astype(np.float32)
+    return np.where(e == 31, big, out)
+
+
+def test_fp16_device_every_pattern(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.fp16_device(h)
+    exp = _fp16_expected(h)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
+    # exponent 0 (both zeros and every subnormal) decodes to +0 bits exactly
+    zeros = got[((h >> 10) & 31) == 0]
+    assert np.all(zeros.view(np.uint32) == 0)
+
+
+def test_fp16_ieee_matches_numpy(oracle):
+    L = O.lib()
+    for h in list(range(0, 65536, 7)) + [0x0001, 0x03FF, 0x8001, 0x7C00, 0xFC00]:
+        want = np.array([h], dtype=np.uint16).view(np.float16).astype(np.float32)[0]
+        got = np.float32(L.oq_fp16_ieee(h))
+        if np.isnan(want):
+            assert np.isnan(got)
+        else:
+            assert got.view(np.uint32) == want.view(np.uint32), hex(h)
+
+
+def test_bf16_rne_matches_torch(oracle):
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, 400_000, dtype=np.uint64).astype(np.uint32)
+    # keep finite values; add exact ties (low half 0x8000) with even and odd keep bits
+    exp = (bits >> 23) & 0xFF
+    bits = bits[exp != 0xFF]
+    ties = (rng.integers(0, 2**16, 50_000, dtype=np.uint32) << 16) | 0x8000
+    ties = ties[((ties >> 23) & 0xFF) < 0xFE]
+    bits = np.concatenate([bits, ties, np.array([0x00000000, 0x80000000, 0x3F808000, 0x3F818000,
+                                                 0x7F7FFFFF & 0x7F7F7FFF], dtype=np.uint32)])
+    f = bits.view(np.float32)
+    want = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = O.bf16_rne(f)
+    assert np.array_equal(got, want)
+
+
+# ---- Appendix-B exhaustiveness: reference device arithmetic == closed form ----
+
+def test_split_hi_lo_is_exact(oracle):
+    assert O.lib().oq_check_split_identity() == 0
+
+
+def test_q_times_d_exhaustive(oracle):
+    """Every normal fp16 d (both signs) x every int8 code: the reference's
+    two-term bf16 scale arithmetic (src/quants/q4_0/unpack.aie.h:41-45,
+    src/quants/q8_0/unpack.aie.h:44-51) rounds to the same bf16 as the closed
+    form. Results that differ only in the sign of a zero are counted apart:
+    they arise for code 0 with negative d, where the two-term sum gives +0."""
+    sz = ctypes.c_int64(0)
+    assert O.lib().oq_check_q_times_d(ctypes.byref(sz)) == 0
+    assert sz.value <= 30720  # at most one per negative normal d (code 0 only)
+
+
+def test_q6_k_exhaustive(oracle):
+    """Every normal fp16 d x every int8 sub-scale x every centred 6-bit code:
+    the reference's three-term split (src/quants/q6_k/unpack.aie.h:33-61,81-91)
+    equals bf16_rne(d * sc * (q - 32))."""
+    sz = ctypes.c_int64(0)
+    assert O.lib().oq_check_q6_k(1, ctypes.byref(sz)) == 0
+
+
+def test_aie_emulation_catches_a_dropped_term(oracle):
+    """The exhaustive check can fail: a one-term scale (hi only, the relaxed
+    mode the reference rejects, src/quants/NOTES.md:327-335) differs from the
+    closed form for some d."""
+    L = O.lib()
+    mism = 0
+    for h in range(0x3C00, 0x3C00 + 1024, 3):  # d in [1, 2)
+        d = np.float32(np.array([h], dtype=np.uint16).view(np.float16)[0])
+        hi = O.bf16_rne(np.array([d], dtype=np.float32)).astype(np.uint32) << 16
+        one_term = O.bf16_rne((np.float32(7) * hi.view(np.float32)).astype(np.float32))[0]
+        if one_term != L.oq_aie_q_times_d(7, h):
+            mism += 1
+    assert mism > 0
+
+
+# ---- dequant closed form vs exact arithmetic --------------------------------
+
+def _fp16_exact(bits):
+    """Exact rational value of the device-decoded scale."""
+    e = (bits >> 10) & 31
+    if e == 0:
+        return Fraction(0)
+    m = bits & 0x3FF
+    s = -1 if bits & 0x8000 else 1
+    return s * Fraction(1024 + m, 1024) * (Fraction(2) ** (e - 15 if e != 31 else 16))
+
+
+def _bf16_of_fraction(v):
+    # exact value -> float32 (exact for these products) -> torch RNE to bf16
+    f = np.array([float(v)], dtype=np.float32)
+    assert Fraction(float(f[0])) == v
+    return int(torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[0])
+
+
+def _exact_block(qtype, blk):
+    """Element values of one canonical block, written from the format
+    description (src/quants/tests/formats/*.py) with exact fractions."""
+    out = []
+    if qtype == O.Q4_0:
+        d = _fp16_exact(int(blk[0]) | (int(blk[1]) << 8))
+        codes = [int(b) & 15 for b in blk[2:18]] + [int(b) >> 4 for b in blk[2:18]]
+        out = [(c - 8) * d for c in codes]
+    elif qtype == O.Q8_0:
+        d = _fp16_exact(int(blk[0]) | (int(blk[1]) << 8))
+        out = [int(np.int8(np.uint8(b))) * d for b in blk[2:34]]
+    else:
+        ql, qh = blk[:128].astype(int), blk[128:192].astype(int)
+        sc = blk[192:208].view(np.int8).astype(int)
+        d = _fp16_exact(int(blk[208]) | (int(blk[209]) << 8))
+        out = [None] * 256
+        for e in range(256):
+            h, r = divmod(e, 128)
+            j, l = divmod(r, 32)
+            byte = ql[64 * h + 32 * (j % 2) + l]
+            nib = (byte >> 4) if j >= 2 else (byte & 15)
+            q = nib | (((qh[32 * h + l] >> (2 * j)) & 3) << 4)
+            out[e] = d * sc[8 * h + l // 16 + 2 * j] * (q - 32)
+    return [_bf16_of_fraction(v) for v in out]
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_dequant_matches_exact_arithmetic(oracle, qtype):
+    rng = np.random.default_rng(qtype)
+    k = O.BLOCK_ELEMS[qtype] * 2
+    n = 3
+    raw = rng.integers(0, 256, n * O.row_bytes(qtype, k), dtype=np.uint8)
+    bb = O.BLOCK_BYTES[qtype]
+    dpos = 0 if qtype != O.Q6_K else 208
+    blocks = raw.reshape(-1, bb)
+    # random but finite-product scales: any fp16 except exponent 31 on most
+    # blocks, plus one block each with exponent 0 and exponent 31
+    dbits = rng.integers(0, 0x7C00, blocks.shape[0]).astype(np.uint16) | (
+        rng.integers(0, 2, blocks.shape[0]).astype(np.uint16) << 15)
+    dbits[0] = 0x0123   # subnormal -> +0
+    dbits[1] = 0x7C05   # exponent 31 -> finite 2^16 * (1 + 5/1024)
+    blocks[:, dpos] = dbits & 0xFF
+    blocks[:, dpos + 1] = dbits >> 8
+    got = O.dequant(qtype, raw, n, k)
+    want = np.array([_exact_block(qtype, b) for b in blocks], dtype=np.uint16).reshape(n, k)
+    # zero results may differ only in sign (see test_q_times_d_exhaustive)
+    both_zero = ((got & 0x7FFF) == 0) & ((want & 0x7FFF) == 0)
+    assert np.array_equal(np.where(both_zero, 0, got), np.where(both_zero, 0, want))
+
+
+def test_golden_special_blocks(oracle):
+    """Hand-computed blocks: every Q4_0 code at d = 1, 0.5, -2, a subnormal d,
+    d = -0 and the exponent-31 quirk; Q8_0 -128..127; Q6_K with known fields."""
+    cases = json.loads((GOLDEN / "special_blocks.json").read_text())
+    for c in cases:
+        qtype = {"q4_0": O.Q4_0, "q8_0": O.Q8_0, "q6_k": O.Q6_K}[c["format"]]
+        raw = np.array(c["block"], dtype=np.uint8)
+        got = O.dequant(qtype, raw, 1, O.BLOCK_ELEMS[qtype])[0]
+        assert got.tolist() == c["bf16"], c["name"]
+
+
+# ---- reference record layout --------------------------------------------------
+
+def _raw_with_specials(qtype, weights_rows, weights_cols, seed):
+    rng = np.random.default_rng(seed)
+    stride = O.row_bytes(qtype, weights_rows)
+    raw = rng.integers(0, 256, weights_cols * stride, dtype=np.uint8)
+    blocks = raw.reshape(-1, O.BLOCK_BYTES[qtype])
+    dpos = 208 if qtype == O.Q6_K else 0
+    blocks[::5, dpos + 1] &= 0x83  # exponent 0 -> subnormal or zero scale
+    return raw, stride
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_ref_repack_matches_reference_build(oracle, qtype):
+    shim = O.ref_shim(qtype)
+    if shim is None:
+        pytest.skip("reference repack not built here (oracle/_ref); fixtures cover it")
+    rows, cols = 512, 24
+    raw, stride = _raw_with_specials(qtype, rows, cols, seed=qtype)
+    for pad in (0, 6):
+        st = stride + pad
+        src = np.zeros(cols * st, dtype=np.uint8)
+        src.reshape(cols, st)[:, :stride] = raw.reshape(cols, stride)
+        want = np.zeros(shim.quants_packed_bytes(rows, cols), dtype=np.uint8)
+        assert shim.quants_repack(src.ctypes.data, st, want.ctypes.data, want.size, rows, cols) == want.size
+        got, warn = O.ref_repack(qtype, src, rows, cols, stride=st)
+        assert np.array_equal(got, want)
+        assert warn & 1
+    # the 0-on-error convention, case by case
+    buf = np.zeros(O.ref_packed_bytes(qtype, rows, cols), dtype=np.uint8)
+    L = O.lib()
+    for (r, c, st, cap) in [(rows, 4, stride, buf.size), (rows - 32, cols, stride, buf.size),
+                            (rows, cols, stride - 2, buf.size), (rows, cols, stride, buf.size - 1),
+                            (0, cols, stride, buf.size), (rows, -8, stride, buf.size)]:
+        a = shim.quants_repack(raw.ctypes.data, st, buf.ctypes.data, cap, r, c)
+        b = L.oq_ref_repack(qtype, raw.ctypes.data, st, buf.ctypes.data, cap, r, c, None)
+        assert a == b == 0
+        assert shim.quants_packed_bytes(r, c) == L.oq_ref_packed_bytes(qtype, r, c)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_ref_repack_matches_fixture(oracle, qtype):
+    fx = np.load(GOLDEN / "ref_records.npz")
+    name = O.FORMAT_NAMES[qtype]
+    raw = fx[f"{name}_raw"]
+    rows, cols = (int(v) for v in fx[f"{name}_shape"])
+    got, _ = O.ref_repack(qtype, raw, rows, cols)
+    assert np.array_equal(got, fx[f"{name}_records"])
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_ref_unpack_equals_canonical_dequant(oracle, qtype):
+    """Decoding the reference's records (its unpack semantics) gives the
+    canonical dequant, re-ordered into the reference output order
+    (src/quants/tests/formats/q4_0.py:65-79)."""
+    rows, cols = 512, 16
+    raw, _ = _raw_with_specials(qtype, rows, cols, seed=10 + qtype)
+    rec, _ = O.ref_repack(qtype, raw, rows, cols)
+    got = O.ref_unpack(qtype, rec, rows, cols)
+    want = O.ref_order(O.dequant(qtype, raw, cols, rows), O.REF_RECORD_ROWS[qtype])
+    both_zero = ((got & 0x7FFF) == 0) & ((want & 0x7FFF) == 0)
+    assert np.array_equal(np.where(both_zero, 0, got), np.where(both_zero, 0, want))
+
+
+# ---- matmul -------------------------------------------------------------------
+
+def test_matmul_f64_matches_numpy(oracle):
+    rng = np.random.default_rng(3)
+    w = O.bf16_rne(rng.standard_normal((40, 96)).astype(np.float32))
+    x = O.bf16_rne(rng.standard_normal((5, 96)).astype(np.float32))
+    wf = (w.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    assert np.allclose(O.matmul_f64(w, x), xf @ wf.T, rtol=1e-12, atol=1e-12)
+    assert np.allclose(O.matmul_f32(w, x), xf @ wf.T, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_quant_matmul_matches_dequant_then_matmul(oracle, qtype):
+    rng = np.random.default_rng(4)
+    n, k = 24, 512
+    raw = rng.integers(0, 256, n * O.row_bytes(qtype, k), dtype=np.uint8)
+    blocks = raw.reshape(-1, O.BLOCK_BYTES[qtype])
+    dpos = 208 if qtype == O.Q6_K else 0
+    blocks[:, dpos + 1] = 0x20  # modest finite scales
+    x = O.bf16_rne(rng.standard_normal((3, k)).astype(np.float32))
+    w = O.dequant(qtype, raw, n, k)
+    ref = O.matmul_f64(w, x)
+    got = O.quant_matmul_f32(qtype, raw, n, k, x, threads=2)
+    assert np.allclose(got, ref, rtol=1e-4, atol=1e-3 * np.abs(ref).max())
