@@ -14,13 +14,12 @@ Measurement
     copies of its weights to exceed the 256 MB Infinity Cache twice over, so
     successive launches read HBM, not the last-level cache.
   - A "step" is one launch of the workload's kernel(s). W warm-up steps, then
-    K steps captured in a HIP graph and replayed once between two
-    synchronizations: whole-job time -> "ms_per_step" and "value".
-  - Kernel duration for the roofline: the same K launches run eagerly with a
-    HIP event pair around each launch on the launch stream, queued behind a
-    spin kernel so that the CPU is ahead of the GPU; the mean of the pairs.
-  - "roofline.achieved" is algorithmic bytes (or FLOPs) per launch divided by
-    that mean. "traffic" comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter
+    K steps captured in a HIP graph and replayed once untimed and once timed.
+    A HIP event pair on the replay stream brackets the timed replay:
+    "ms_per_step" is its duration / K, "value" is K steps of algorithmic work
+    over it (whole-job throughput, inputs resident in HBM), and
+    "roofline.achieved" is the algorithmic bytes (or FLOPs) of one launch over
+    the mean step. "wall_ms_per_step" is the host clock around the same replay. "traffic" comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter
     runs recorded in profiles/traffic.json when present.
   - "cpu_baseline": the CPU oracle's streaming dequantize-and-multiply over the
     same canonical Q8_0 tensor, on the host's cores, repeated for ~10 s.
@@ -59,38 +58,38 @@ def copies_for(bytes_per_step):
 
 
 class Timer:
+    """W eager warm-up launches, then K launches captured in one HIP graph.
+
+    The graph is replayed once untimed (upload), then once timed: a HIP event
+    pair on the replay stream brackets the K launches, between two device
+    synchronizations. Returns (wall seconds, event seconds) of the timed
+    replay; event seconds / K is the mean duration of one step."""
+
     def __init__(self, torch):
         self.torch = torch
 
     def run(self, launch, steps, warmup):
         torch = self.torch
-        stream = torch.cuda.current_stream()
         for i in range(warmup):
             launch(i)
         torch.cuda.synchronize()
-        # Whole-job: K launches in one graph, replayed once.
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for i in range(steps):
                 launch(i)
-        g.replay()  # first replay uploads the graph
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         g.replay()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        # Kernel duration: per-launch event pairs queued behind a spin kernel.
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        torch.cuda._sleep(int(2e7))
-        for i in range(steps):
-            starts[i].record(stream)
-            launch(i)
-            ends[i].record(stream)
+        stream = torch.cuda.current_stream()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record(stream)
+        g.replay()
+        end.record(stream)
         torch.cuda.synchronize()
-        durs = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)]) * 1e-3  # seconds
+        wall = time.perf_counter() - t0
         del g
-        return wall, durs
+        return wall, start.elapsed_time(end) * 1e-3
 
 
 def traffic_table():
@@ -134,13 +133,12 @@ def main():
         x = synth.make_x(m, k, seed)
         return x, torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(dev)
 
-    def record(name, wall, durs, per_launch, unit, peak, bound, extra=None):
-        mean = float(np.mean(durs))
-        achieved = per_launch / mean / (1e9 if unit == "GB/s" else 1e12)
-        whole = per_launch * steps / wall / (1e9 if unit == "GB/s" else 1e12)
-        r = {"value": whole, "unit": unit, "ms_per_step": wall / steps * 1e3,
-             "kernel_us_mean": mean * 1e6, "kernel_us_p10": float(np.percentile(durs, 10)) * 1e6,
-             "kernel_us_p90": float(np.percentile(durs, 90)) * 1e6,
+    def record(name, wall, ev, per_launch, unit, peak, bound, extra=None):
+        scale = 1e9 if unit == "GB/s" else 1e12
+        step = ev / steps
+        achieved = per_launch / step / scale
+        r = {"value": per_launch * steps / ev / scale, "unit": unit, "ms_per_step": step * 1e3,
+             "wall_ms_per_step": wall / steps * 1e3, "step_us": step * 1e6,
              "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                           "frac": achieved / peak}}
         if extra:
@@ -156,8 +154,8 @@ def main():
         raw, ws = upload_planar(TYPE_Q8_0, n, k, 1, copies_for(wbytes))
         x, xd = x_dev(1, k, 2)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q8_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("gemv_q8_0", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q8_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q8_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q8_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         cpu_raw, cpu_x = raw, x
@@ -170,8 +168,8 @@ def main():
         _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies_for(wbytes))
         _, xd = x_dev(1, k, 4)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q6_K, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("gemv_q6_k", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q6_K, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q6_k", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q6_K decode GEMV y[4096] = W[4096x14336] x[14336], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
@@ -183,8 +181,8 @@ def main():
         _, ws = upload_planar(TYPE_Q4_0, n, k, 5, copies_for(wbytes))
         _, xd = x_dev(1, k, 6)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("gemv_q4_0", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 decode GEMV y[4096] = W[4096x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
@@ -197,12 +195,12 @@ def main():
         copies = copies_for(inb + outb)
         _, ws = upload_planar(TYPE_Q4_0, n, k, 0, copies)
         outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
-        wall, durs = timer.run(lambda i: ops.dequant(TYPE_Q4_0, ws[i % copies], n, k, out=outs[i % copies]),
+        wall, ev = timer.run(lambda i: ops.dequant(TYPE_Q4_0, ws[i % copies], n, k, out=outs[i % copies]),
                                steps, warmup)
-        record("dequant_q4_0", wall, durs, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
+        record("dequant_q4_0", wall, ev, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 -> bf16 dequant, 4096x4096 (524,288 blocks)",
                 "bytes_per_launch": inb + outb, "packed_bytes": inb, "copies": copies})
-        results["dequant_q4_0"]["packed_GBps"] = inb / np.mean(durs) / 1e9
+        results["dequant_q4_0"]["packed_GBps"] = inb / (ev / steps) / 1e9
         del ws, outs
 
     # --- Q4_0 dequant-GEMM, M = 512 ---------------------------------------------
@@ -214,9 +212,9 @@ def main():
         xs = [x_dev(m, k, 8 + c)[1] for c in range(copies)]
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         flops = 2.0 * m * n * k
-        wall, durs = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y),
+        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y),
                                steps, warmup)
-        record("gemm_q4_0", wall, durs, flops, "TFLOP/s", MFMA_BF16_PEAK_TFS, "mfma",
+        record("gemm_q4_0", wall, ev, flops, "TFLOP/s", MFMA_BF16_PEAK_TFS, "mfma",
                {"workload": "Q4_0 prefill dequant-GEMM Y[512x4096] = X[512x4096] W[4096x4096]^T, bf16 MFMA, fp32 acc",
                 "flops_per_launch": flops, "copies": copies})
         del ws, xs
@@ -261,14 +259,14 @@ def main():
             ops.mul_mat_id(TYPE_Q4_0, gus[c], gu_per, n_expert, inter2, hidden, x1, ids_d, workspace=ws1, out=y1)
             ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, x2, ids_d, workspace=ws2, out=y2)
 
-        wall, durs = timer.run(launch, steps, warmup)
+        wall, ev = timer.run(launch, steps, warmup)
         wbytes = touched * (gu_per + dn_per)
         flops = 2.0 * n_tokens * top_k * (inter2 * hidden + hidden * inter)
-        record("moe_q4_0", wall, durs, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        record("moe_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 MoE: 128 experts (gate_up 1536x2048, down 2048x768), 64 tokens, top-8; "
                             "one step = gate_up + down MUL_MAT_ID",
                 "bytes_per_launch": wbytes, "touched_experts": int(touched),
-                "tflops": flops / float(np.mean(durs)) / 1e12, "copies": copies})
+                "tflops": flops / (ev / steps) / 1e12, "copies": copies})
         del gus, dns
 
     if not results:

@@ -63,11 +63,11 @@ struct PlanarQ6_K {
 // Block-scale decode with the reference's device rule
 // (src/quants/common/scale.aie.h:14-27): exponent 0 (zero or subnormal) gives
 // +0, exponent 31 gives the finite 2^16 * (1.m), otherwise IEEE binary16.
+// Written as an integer select so it compiles to v_cndmask, not a branch.
 __device__ __forceinline__ float fp16_scale(uint32_t h) {
-  const uint32_t e = (h >> 10) & 31u;
-  const uint32_t bits =
-      ((h & 0x8000u) << 16) | ((e + 112u) << 23) | ((h & 0x3ffu) << 13);
-  return e ? __uint_as_float(bits) : 0.0f;
+  const uint32_t e = h & 0x7c00u;
+  const uint32_t bits = ((h & 0x8000u) << 16) | (((h & 0x7fffu) << 13) + 0x38000000u);
+  return __uint_as_float(e ? bits : 0u);
 }
 
 // Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even.

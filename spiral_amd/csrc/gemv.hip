@@ -4,32 +4,50 @@
 // M = 1: src/quants/q4_0/mmul.aie.h:16-90, src/quants/q8_0/mmul.aie.h:16-117,
 // src/quants/q6_k/mmul.aie.h:18-84).
 //
-// Structure
-//  - A workgroup of 4 waves stages x once into LDS in the form its format's
-//    inner loop wants (see stage_x), then walks rows persistently: wave w of
-//    workgroup g takes row groups w + 4g, w + 4g + 4*gridDim, ...
-//  - A "task" is the unit one lane consumes per 16-byte payload load(s):
-//      Q4_0: one block (16 B qs + fp16 d) = 32 weights
-//      Q8_0: half a block (16 B qs + d)   = 16 weights
-//      Q6_K: a quarter super-block (2x16 B ql + 16 B qh + 4 sub-scales + d)
-//            = 64 weights
-//    Lane l of a wave takes tasks l, l + 64, ... of its row group, so every
-//    payload load instruction of the wave reads 1 KiB of contiguous bytes.
-//  - Each lane keeps an fp32 partial sum per row; a wave butterfly reduction
-//    finishes the row.
+// Work split
+//  - A workgroup of WAVES waves stages x once into LDS in the form its
+//    format's inner loop reads. Each wave owns a contiguous, balanced range
+//    of rows; row indices are wave-uniform (scalar registers), so payload
+//    addresses are a scalar row base plus a 32-bit lane offset.
+//  - A row is cut into T "tasks", the unit one lane consumes per 16-byte
+//    payload load(s):
+//      Q4_0: one block (16 B qs + fp16 d)                          = 32 weights
+//      Q8_0: half a block (16 B qs + d)                            = 16 weights
+//      Q6_K: a quarter super-block (2x16 B ql, 16 B qh, 4 sub-scales, d)
+//                                                                  = 64 weights
+//    A "unit" is J tasks per lane: tasks 64 J p + 64 j + lane of a row (pass
+//    p). Each payload load instruction of a wave reads 1 KiB of contiguous
+//    bytes. When one pass covers the row (T <= 64 J), every lane's x slice is
+//    the same for all rows and lives in registers (XREG); otherwise it is
+//    read from LDS per unit.
+//  - Units are software-pipelined: the payload of unit u + 1 is in flight
+//    while unit u is computed, and the first unit is requested before x is
+//    staged, so the HBM latency of the first loads overlaps the staging.
+//  - LDS holds x in 16-byte entries blocked by 64 tasks: entry e of task t
+//    sits at ((t / 64) E + e) KiB + (t % 64) 16 bytes, so a wave reading
+//    entry e of its 64 tasks touches 1 KiB of consecutive LDS and e is an
+//    immediate offset. Per-task sums of x follow the entries.
+//  - A row's fp32 partial sums are reduced across the wave after its last
+//    pass and lane 0 stores y.
 //
 // Arithmetic (fp32 accumulation throughout):
-//  - Codes are used in an unsigned offset form and the offset is removed once
-//    per task with a precomputed sum of x over the task's k range:
-//      sum (q - c) x = sum q' x - c' * sum x.
-//  - Q4_0 builds bf16 pairs (128 + q) straight from the nibbles with one
-//    and-or each and multiplies them against bf16 x pairs with
-//    v_dot2_f32_bf16; Q8_0 and Q6_K convert codes with v_cvt_f32_ubyte and
-//    use fp32 FMAs against fp32 x.
+//  - Codes are turned into small floats with an exact offset and the offset
+//    is removed once per task with a precomputed sum of x over the task:
+//      sum (q - c) x = sum (q + B) x - (B + c) * sum x.
+//  - Q4_0 and Q6_K form their codes bytewise (nibble masks; Q6_K adds the
+//    two high bits), then bf16 pairs (128 + code) of consecutive elements
+//    with one v_perm_b32 each (code byte low, 0x43 high), and multiply them
+//    against bf16 x pairs with v_dot2_f32_bf16. x is staged unchanged.
+//  - Q8_0 codes (q + 128 up to 255) do not fit a bf16 mantissa; it builds
+//    fp16 pairs (1024 + q + 128) with one v_perm_b32 each (0x64 high) and
+//    multiplies each half against fp32 x with v_fma_mix_f32 (the fp16
+//    operand is widened exactly inside the FMA).
 //  - Weights are not rounded to bf16 first (the block scale multiplies the
 //    block sum), so results differ from the bf16-weight product by rounding
 //    only; tests bound that difference.
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 
 #include "common.h"
 
@@ -37,333 +55,541 @@ namespace spiral {
 namespace {
 
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
 
-constexpr int kGemvWaves = 4;
-constexpr int kGemvThreads = 64 * kGemvWaves;
+constexpr int64_t kMaxLds = 64 * 1024;
 
-template <int TYPE>
-struct GemvTraits;
-
-// Q4_0: task = one block. LDS: x as bf16 pairs permuted to the nibble order
-// of the and-or extraction (16 pairs per block), then one fp32 x-sum per block.
-template <>
-struct GemvTraits<SPIRAL_TYPE_Q4_0> {
-  static __host__ __device__ int64_t tasks_per_row(int64_t k) { return k / 32; }
-  static __host__ __device__ int64_t lds_bytes(int64_t k) { return k * 2 + (k / 32) * 4; }
-};
-// Q8_0: task = 16 codes. LDS: fp32 x, then one fp32 sum per 16 elements.
-template <>
-struct GemvTraits<SPIRAL_TYPE_Q8_0> {
-  static __host__ __device__ int64_t tasks_per_row(int64_t k) { return k / 16; }
-  static __host__ __device__ int64_t lds_bytes(int64_t k) { return k * 4 + (k / 16) * 4; }
-};
-// Q6_K: task = 64 codes (h, 16-lane half). LDS as Q8_0.
-template <>
-struct GemvTraits<SPIRAL_TYPE_Q6_K> {
-  static __host__ __device__ int64_t tasks_per_row(int64_t k) { return k / 64; }
-  static __host__ __device__ int64_t lds_bytes(int64_t k) { return k * 4 + (k / 16) * 4; }
-};
-
-// ---- x staging ---------------------------------------------------------------
-
-template <int TYPE>
-__device__ void stage_x(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
-  if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
-    // Block b's 32 x values become 16 bf16 pairs, in the order the task loop
-    // consumes them: for qs dword i (bytes 4i..4i+3) the pairs
-    // (x[4i], x[4i+2]) (x[4i+16], x[4i+18]) (x[4i+1], x[4i+3])
-    // (x[4i+17], x[4i+19]) match nibble fields at bit offsets 0, 4, 8, 12.
-    uint32_t* pairs = reinterpret_cast<uint32_t*>(lds);
-    float* sums = reinterpret_cast<float*>(lds + k * 2);
-    const int64_t nb = k / 32;
-    for (int64_t b = threadIdx.x; b < nb; b += blockDim.x) {
-      const uint4* src = reinterpret_cast<const uint4*>(x + b * 32);
-      uint32_t v[16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 t = src[j];
-        v[4 * j + 0] = t.x; v[4 * j + 1] = t.y; v[4 * j + 2] = t.z; v[4 * j + 3] = t.w;
-      }
-      // v[m] holds x[2m] (low half) and x[2m+1] (high half).
-      auto xe = [&](int e) -> uint32_t { return (e & 1) ? (v[e >> 1] >> 16) : (v[e >> 1] & 0xffffu); };
-      float s = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 32; ++e) s += __uint_as_float(xe(e) << 16);
-      uint4* dst = reinterpret_cast<uint4*>(pairs + b * 16);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        dst[i] = make_uint4(xe(4 * i) | (xe(4 * i + 2) << 16), xe(4 * i + 16) | (xe(4 * i + 18) << 16),
-                            xe(4 * i + 1) | (xe(4 * i + 3) << 16), xe(4 * i + 17) | (xe(4 * i + 19) << 16));
-      }
-      sums[b] = s;
-    }
-  } else {
-    float* xf = reinterpret_cast<float*>(lds);
-    float* sums = reinterpret_cast<float*>(lds + k * 4);
-    const int64_t nc = k / 16;
-    for (int64_t c = threadIdx.x; c < nc; c += blockDim.x) {
-      const uint4* src = reinterpret_cast<const uint4*>(x + c * 16);
-      const uint4 a = src[0], b = src[1];
-      const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      float f[16];
-      float s = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        f[2 * j] = bf16_lo(w[j]);
-        f[2 * j + 1] = bf16_hi(w[j]);
-        s += f[2 * j] + f[2 * j + 1];
-      }
-      float4* dst = reinterpret_cast<float4*>(xf + c * 16);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) dst[j] = make_float4(f[4 * j], f[4 * j + 1], f[4 * j + 2], f[4 * j + 3]);
-      sums[c] = s;
-    }
-  }
+// fp16 pairs (1024 + byte b0, 1024 + byte b2) and (1024 + b1, 1024 + b3) of
+// a dword: bytes [b, 0x64] form the fp16 0x6400 | b.
+__device__ __forceinline__ f16x2_t f16_even(uint32_t w) {
+  return __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x04020400u));
+}
+__device__ __forceinline__ f16x2_t f16_odd(uint32_t w) {
+  return __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, w, 0x04030401u));
 }
 
-// ---- per-task payload and compute -------------------------------------------
+// sum over the 4 bytes of w (as 1024 + byte) times x[0..3], two chains.
+__device__ __forceinline__ void mix4(uint32_t w, float x0, float x1, float x2, float x3, float& s0, float& s1) {
+  const f16x2_t e = f16_even(w), o = f16_odd(w);
+  s0 = __builtin_fmaf(static_cast<float>(e.x), x0, s0);
+  s1 = __builtin_fmaf(static_cast<float>(o.x), x1, s1);
+  s0 = __builtin_fmaf(static_cast<float>(e.y), x2, s0);
+  s1 = __builtin_fmaf(static_cast<float>(o.y), x3, s1);
+}
+
+// bf16 pairs (128 + b0, 128 + b1) and (128 + b2, 128 + b3) of a dword of
+// bytes below 128: bytes [b, 0x43] form the bf16 0x4300 | b.
+__device__ __forceinline__ uint32_t bf16_01(uint32_t w) { return __builtin_amdgcn_perm(0x43434343u, w, 0x04010400u); }
+__device__ __forceinline__ uint32_t bf16_23(uint32_t w) { return __builtin_amdgcn_perm(0x43434343u, w, 0x04030402u); }
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// Blocked LDS layout (see the header): byte offset of entry 0 of task t when
+// a task has E 16-byte entries; entry e adds e KiB.
+__host__ __device__ __forceinline__ uint32_t lds_task(int t, int E) {
+  return static_cast<uint32_t>((t >> 6) * E) * 1024u + (static_cast<uint32_t>(t & 63) << 4);
+}
+__host__ __device__ __forceinline__ int64_t pad64(int64_t t) { return (t + 63) & ~int64_t(63); }
 
 template <int TYPE>
-struct Task;
+struct Fmt;
 
+// Staging: every workgroup copies x into LDS once. Items are handed out to
+// threads K_STAGE at a time with all of an item's global loads issued before
+// any is used, so a thread has up to K_STAGE * 32 bytes of x in flight.
+constexpr int kStageUnroll = 4;
+
+// ---- Q4_0 ------------------------------------------------------------------
+// x entries per task (block): 4 x uint4 = its 32 bf16 x in order. Sum: float.
+// Codes: for qs dword i, the low nibbles are elements 4i..4i+3 and the high
+// nibbles elements 16+4i..16+4i+3; masked to bytes and widened to bf16 pairs
+// (128 + c) with v_perm they line up with consecutive x pairs.
 template <>
-struct Task<SPIRAL_TYPE_Q4_0> {
-  uint4 q;
-  uint32_t d;
-  __device__ __forceinline__ void load(const PlanarQ4_0& P, int64_t blk) {
-    q = load_stream16(reinterpret_cast<const uint4*>(P.qs) + blk);
-    d = P.d[blk];
+struct Fmt<SPIRAL_TYPE_Q4_0> {
+  static constexpr int kTaskElems = 32, kE = 4;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 4); }
+
+  struct Row {
+    const uint8_t* qs;
+    const uint8_t* d;
+  };
+  static __device__ __forceinline__ Row row(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r) {
+    const int64_t nb = k / 32;
+    return Row{w + r * nb * 16, w + n_rows * nb * 16 + r * nb * 2};
   }
-  __device__ __forceinline__ float compute(const uint8_t* lds, int64_t k, int64_t t) const {
-    const uint4* xp = reinterpret_cast<const uint4*>(lds) + t * 4;
-    const float xs = reinterpret_cast<const float*>(lds + k * 2)[t];
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  struct Payload {
+    uint4 q;
+    uint32_t d;
+  };
+  static __device__ __forceinline__ void load(Payload& p, const Row& R, int t) {
+    const uint32_t ut = static_cast<uint32_t>(t);
+    p.q = load_stream16(R.qs + ut * 16u);
+    p.d = *reinterpret_cast<const uint16_t*>(R.d + ut * 2u);
+  }
+  struct X {
+    uint4 xp[4];
+    float sum;
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) {
+    const uint8_t* e = lds + lds_task(t, kE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.xp[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+    x.sum = reinterpret_cast<const float*>(lds + pad64(T) * kE * 16)[t];
+  }
+  // Item = task: 32 x (4 x 16 B) and their sum.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const int T = static_cast<int>(k / 32);
+    float* xs = reinterpret_cast<float*>(lds + pad64(T) * kE * 16);
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    for (int b0 = threadIdx.x; b0 < T; b0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll][4];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int b = b0 + u * blockDim.x;
+        if (b < T)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[u][i] = src[4 * b + i];
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int b = b0 + u * blockDim.x;
+        if (b >= T) break;
+        float s = 0.0f;
+        uint8_t* dst = lds + lds_task(b, kE);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 q = v[u][i];
+          s += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
+               (bf16_lo(q.w) + bf16_hi(q.w));
+          *reinterpret_cast<uint4*>(dst + 1024 * i) = q;
+        }
+        xs[b] = s;
+      }
+    }
+  }
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
     float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint4 xv = xp[i];
-      const uint32_t m = 0x000F000Fu, o = 0x43004300u;
-      const uint32_t t0 = (w[i] & m) | o;
-      const uint32_t t1 = ((w[i] >> 4) & m) | o;
-      const uint32_t t2 = ((w[i] >> 8) & m) | o;
-      const uint32_t t3 = ((w[i] >> 12) & m) | o;
-      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t0), __builtin_bit_cast(bf16x2_t, xv.x), s0, false);
-      s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t1), __builtin_bit_cast(bf16x2_t, xv.y), s1, false);
-      s0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t2), __builtin_bit_cast(bf16x2_t, xv.z), s0, false);
-      s1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, t3), __builtin_bit_cast(bf16x2_t, xv.w), s1, false);
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
+      s0 = dot2(bf16_01(lo), (i & 1) ? el.z : el.x, s0);
+      s1 = dot2(bf16_23(lo), (i & 1) ? el.w : el.y, s1);
+      s0 = dot2(bf16_01(hi), (i & 1) ? eh.z : eh.x, s0);
+      s1 = dot2(bf16_23(hi), (i & 1) ? eh.w : eh.y, s1);
     }
-    // bf16 (128 + q) against x: remove 136 * sum(x) to get sum (q - 8) x.
-    return fp16_scale(d) * ((s0 + s1) - 136.0f * xs);
+    // bf16 (128 + c) against x: remove 136 * sum(x) to get sum (c - 8) x.
+    return fp16_scale(p.d) * ((s0 + s1) - 136.0f * x.sum);
   }
 };
 
+// ---- Q8_0 ------------------------------------------------------------------
+// x entries per task (half block): 4 x float4 = its 16 x. Sum: float.
 template <>
-struct Task<SPIRAL_TYPE_Q8_0> {
-  uint4 q;
-  uint32_t d;
-  __device__ __forceinline__ void load(const PlanarQ8_0& P, int64_t blk2) {
-    q = load_stream16(reinterpret_cast<const uint4*>(P.qs) + blk2);
-    d = P.d[blk2 >> 1];
+struct Fmt<SPIRAL_TYPE_Q8_0> {
+  static constexpr int kTaskElems = 16, kE = 4;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 16) * (kE * 16 + 4); }
+
+  struct Row {
+    const uint8_t* qs;
+    const uint8_t* d;
+  };
+  static __device__ __forceinline__ Row row(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r) {
+    const int64_t nb = k / 32;
+    return Row{w + r * nb * 32, w + n_rows * nb * 32 + r * nb * 2};
   }
-  __device__ __forceinline__ float compute(const uint8_t* lds, int64_t k, int64_t t) const {
-    const float4* xp = reinterpret_cast<const float4*>(lds) + t * 4;
-    const float xs = reinterpret_cast<const float*>(lds + k * 4)[t];
-    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+  struct Payload {
+    uint4 q;
+    uint32_t d;
+  };
+  static __device__ __forceinline__ void load(Payload& p, const Row& R, int t) {
+    const uint32_t ut = static_cast<uint32_t>(t);
+    p.q = load_stream16(R.qs + ut * 16u);
+    p.d = *reinterpret_cast<const uint16_t*>(R.d + (ut >> 1) * 2u);
+  }
+  struct X {
+    float4 x[4];
+    float sum;
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) {
+    const uint8_t* e = lds + lds_task(t, kE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.x[i] = *reinterpret_cast<const float4*>(e + 1024 * i);
+    x.sum = reinterpret_cast<const float*>(lds + pad64(T) * kE * 16)[t];
+  }
+  // Item = task: 16 x (2 x 16 B) widened to fp32, and their sum.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const int T = static_cast<int>(k / 16);
+    float* xs = reinterpret_cast<float*>(lds + pad64(T) * kE * 16);
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    for (int c0 = threadIdx.x; c0 < T; c0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll][2];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int c = c0 + u * blockDim.x;
+        if (c < T) {
+          v[u][0] = src[2 * c];
+          v[u][1] = src[2 * c + 1];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int c = c0 + u * blockDim.x;
+        if (c >= T) break;
+        const uint32_t w[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w, v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
+        float s = 0.0f;
+        uint8_t* dst = lds + lds_task(c, kE);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float4 f = make_float4(bf16_lo(w[2 * i]), bf16_hi(w[2 * i]), bf16_lo(w[2 * i + 1]), bf16_hi(w[2 * i + 1]));
+          s += (f.x + f.y) + (f.z + f.w);
+          *reinterpret_cast<float4*>(dst + 1024 * i) = f;
+        }
+        xs[c] = s;
+      }
+    }
+  }
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    // (q ^ 0x80) read as unsigned is q + 128; as fp16 1024 + q + 128.
+    const uint32_t w[4] = {p.q.x ^ 0x80808080u, p.q.y ^ 0x80808080u, p.q.z ^ 0x80808080u, p.q.w ^ 0x80808080u};
     float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float4 xv = xp[i];
-      // (q ^ 0x80) read as unsigned is q + 128.
-      s0 = __builtin_fmaf(static_cast<float>(w[i] & 0xffu), xv.x, s0);
-      s1 = __builtin_fmaf(static_cast<float>((w[i] >> 8) & 0xffu), xv.y, s1);
-      s0 = __builtin_fmaf(static_cast<float>((w[i] >> 16) & 0xffu), xv.z, s0);
-      s1 = __builtin_fmaf(static_cast<float>(w[i] >> 24), xv.w, s1);
-    }
-    return fp16_scale(d) * ((s0 + s1) - 128.0f * xs);
+    for (int i = 0; i < 4; ++i) mix4(w[i], x.x[i].x, x.x[i].y, x.x[i].z, x.x[i].w, s0, s1);
+    return fp16_scale(p.d) * ((s0 + s1) - 1152.0f * x.sum);
   }
 };
 
+// ---- Q6_K ------------------------------------------------------------------
+// Task u of a row = super-block u / 4, half h = (u >> 1) & 1, 16-lane half
+// s = u & 1: elements 128 h + 32 j + 16 s + i for group j < 4, i < 16.
+// x entries per task: 8 x uint4; entry 2 j + (i / 8) holds the 8 bf16 x of
+// group j at i / 8 * 8 .. + 7, in order. Sum: float4, one per group.
 template <>
-struct Task<SPIRAL_TYPE_Q6_K> {
-  uint4 a, b, h;
-  uint2 sc;
-  uint32_t d;
-  int half16;  // 0 or 1: which 16-element half of the 32-lane l range
-  __device__ __forceinline__ void load(const PlanarQ6_K& P, int64_t sb, int u) {
-    // u = 2*h + half: elements 128h + 32j + 16*half + i, i < 16, j < 4.
-    const int hh = u >> 1;
-    half16 = u & 1;
-    const uint8_t* ql = P.ql + sb * 128 + 64 * hh + 16 * half16;
-    a = load_stream16(ql);       // j = 0 (low), 2 (high)
-    b = load_stream16(ql + 32);  // j = 1 (low), 3 (high)
-    h = load_stream16(P.qh + sb * 64 + 32 * hh + 16 * half16);
-    sc = *reinterpret_cast<const uint2*>(P.sc + sb * 16 + 8 * hh);
-    d = P.d[sb];
+struct Fmt<SPIRAL_TYPE_Q6_K> {
+  static constexpr int kTaskElems = 64, kE = 8;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 64) * (kE * 16 + 16); }
+
+  struct Row {
+    const uint8_t* ql;
+    const uint8_t* qh;
+    const uint8_t* sc;
+    const uint8_t* d;
+  };
+  static __device__ __forceinline__ Row row(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r) {
+    const int64_t nb = k / 256, tot = n_rows * nb;
+    return Row{w + r * nb * 128, w + tot * 128 + r * nb * 64, w + tot * 192 + r * nb * 16, w + tot * 208 + r * nb * 2};
   }
-  __device__ __forceinline__ float compute(const uint8_t* lds, int64_t k, int64_t kbase) const {
-    // kbase = first element of j = 0; j adds 32.
-    const float* xf = reinterpret_cast<const float*>(lds);
-    const float* xs = reinterpret_cast<const float*>(lds + k * 4);
-    const uint32_t A[4] = {a.x, a.y, a.z, a.w}, B[4] = {b.x, b.y, b.z, b.w}, H[4] = {h.x, h.y, h.z, h.w};
+  struct Payload {
+    uint4 a, b, h;
+    uint32_t sc;  // the four sub-scales of the task's groups, one per byte
+    uint32_t d;
+  };
+  static __device__ __forceinline__ void load(Payload& p, const Row& R, int u) {
+    const uint32_t uu = static_cast<uint32_t>(u);
+    const uint32_t sb = uu >> 2, hh = (uu >> 1) & 1u, s = uu & 1u;
+    const uint32_t lo = sb * 128u + 64u * hh + 16u * s;
+    p.a = load_stream16(R.ql + lo);        // groups 0 (low nibbles) and 2 (high)
+    p.b = load_stream16(R.ql + lo + 32u);  // groups 1 (low) and 3 (high)
+    p.h = load_stream16(R.qh + sb * 64u + 32u * hh + 16u * s);
+    // Sub-scale of group j is sc[8 h + s + 2 j]: bytes s, s+2, s+4, s+6 of
+    // the 8 sub-scales of half h.
+    const uint2 sc8 = *reinterpret_cast<const uint2*>(R.sc + sb * 16u + 8u * hh);
+    const uint32_t l = s ? (sc8.x >> 8) : sc8.x, hi = s ? (sc8.y >> 8) : sc8.y;
+    p.sc = __builtin_amdgcn_perm(hi, l, 0x06040200u);
+    p.d = *reinterpret_cast<const uint16_t*>(R.d + sb * 2u);
+  }
+  struct X {
+    uint4 x[8];
+    float4 sum;
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int u) {
+    const uint8_t* e = lds + lds_task(u, kE);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.x[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+    x.sum = reinterpret_cast<const float4*>(lds + pad64(T) * kE * 16)[u];
+  }
+  // Item = (task, group): 16 x (2 x 16 B) and their sum.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const int T = static_cast<int>(k / 64);
+    float* xs = reinterpret_cast<float*>(lds + pad64(T) * kE * 16);
+    const int items = 4 * T;
+    for (int e0 = threadIdx.x; e0 < items; e0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll][2];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int e = e0 + u * blockDim.x;
+        if (e < items) {
+          const int t = e >> 2, j = e & 3;
+          const uint4* src = reinterpret_cast<const uint4*>(
+              x + (t >> 2) * 256 + ((t >> 1) & 1) * 128 + (t & 1) * 16 + 32 * j);
+          v[u][0] = src[0];
+          v[u][1] = src[1];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int e = e0 + u * blockDim.x;
+        if (e >= items) break;
+        const int t = e >> 2, j = e & 3;
+        float s = 0.0f;
+        uint8_t* dst = lds + lds_task(t, kE) + 1024 * (2 * j);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const uint4 q = v[u][i];
+          s += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
+               (bf16_lo(q.w) + bf16_hi(q.w));
+          *reinterpret_cast<uint4*>(dst + 1024 * i) = q;
+        }
+        xs[e] = s;
+      }
+    }
+  }
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const uint32_t A[4] = {p.a.x, p.a.y, p.a.z, p.a.w}, B[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
+    const uint32_t H[4] = {p.h.x, p.h.y, p.h.z, p.h.w};
     float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t q[4] = {
-          (A[i] & 0x0F0F0F0Fu) | ((H[i] << 4) & 0x30303030u),
-          (B[i] & 0x0F0F0F0Fu) | ((H[i] << 2) & 0x30303030u),
-          ((A[i] >> 4) & 0x0F0F0F0Fu) | (H[i] & 0x30303030u),
-          ((B[i] >> 4) & 0x0F0F0F0Fu) | ((H[i] >> 2) & 0x30303030u),
+    for (int q = 0; q < 4; ++q) {
+      // 6-bit codes of elements 4q .. 4q+3 of each group, one per byte.
+      const uint32_t c[4] = {
+          (A[q] & 0x0F0F0F0Fu) | ((H[q] << 4) & 0x30303030u),
+          (B[q] & 0x0F0F0F0Fu) | ((H[q] << 2) & 0x30303030u),
+          ((A[q] >> 4) & 0x0F0F0F0Fu) | (H[q] & 0x30303030u),
+          ((B[q] >> 4) & 0x0F0F0F0Fu) | ((H[q] >> 2) & 0x30303030u),
       };
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float4 xv = *reinterpret_cast<const float4*>(xf + kbase + 32 * j + 4 * i);
-        s[j] = __builtin_fmaf(static_cast<float>(q[j] & 0xffu), xv.x, s[j]);
-        s[j] = __builtin_fmaf(static_cast<float>((q[j] >> 8) & 0xffu), xv.y, s[j]);
-        s[j] = __builtin_fmaf(static_cast<float>((q[j] >> 16) & 0xffu), xv.z, s[j]);
-        s[j] = __builtin_fmaf(static_cast<float>(q[j] >> 24), xv.w, s[j]);
+        const uint4 xv = x.x[2 * j + (q >> 1)];
+        s[j] = dot2(bf16_01(c[j]), (q & 1) ? xv.z : xv.x, s[j]);
+        s[j] = dot2(bf16_23(c[j]), (q & 1) ? xv.w : xv.y, s[j]);
       }
     }
-    // Sub-scale of group j is sc[8h + half + 2j]: bytes half, half+2, half+4,
-    // half+6 of the 8 sub-scales loaded for this h.
-    const uint32_t s0 = half16 ? (sc.x >> 8) : sc.x;
-    const uint32_t s1 = half16 ? (sc.y >> 8) : sc.y;
-    const float c0 = static_cast<float>(static_cast<int8_t>(s0 & 0xffu));
-    const float c1 = static_cast<float>(static_cast<int8_t>((s0 >> 16) & 0xffu));
-    const float c2 = static_cast<float>(static_cast<int8_t>(s1 & 0xffu));
-    const float c3 = static_cast<float>(static_cast<int8_t>((s1 >> 16) & 0xffu));
-    const int64_t c16 = kbase >> 4;
-    float acc = c0 * (s[0] - 32.0f * xs[c16]);
-    acc = __builtin_fmaf(c1, s[1] - 32.0f * xs[c16 + 2], acc);
-    acc = __builtin_fmaf(c2, s[2] - 32.0f * xs[c16 + 4], acc);
-    acc = __builtin_fmaf(c3, s[3] - 32.0f * xs[c16 + 6], acc);
-    return fp16_scale(d) * acc;
+    // bf16 (128 + code) against x: remove (128 + 32) * sum(x) per group.
+    const float c0 = static_cast<float>(static_cast<int8_t>(p.sc & 0xffu));
+    const float c1 = static_cast<float>(static_cast<int8_t>((p.sc >> 8) & 0xffu));
+    const float c2 = static_cast<float>(static_cast<int8_t>((p.sc >> 16) & 0xffu));
+    const float c3 = static_cast<float>(static_cast<int8_t>(p.sc >> 24));
+    float acc = c0 * (s[0] - 160.0f * x.sum.x);
+    acc = __builtin_fmaf(c1, s[1] - 160.0f * x.sum.y, acc);
+    acc = __builtin_fmaf(c2, s[2] - 160.0f * x.sum.z, acc);
+    acc = __builtin_fmaf(c3, s[3] - 160.0f * x.sum.w, acc);
+    return fp16_scale(p.d) * acc;
   }
 };
 
-// One lane's task: where it is and its loaded payload.
-template <int TYPE>
-struct Slot {
-  Task<TYPE> task;
-  int64_t t;  // task index within its row
-  __device__ __forceinline__ void load(const void* w, int64_t n_rows, int64_t nb, int64_t n,
-                                       int64_t t_) {
-    t = t_;
-    if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
-      task.load(PlanarQ4_0(w, n_rows, nb), n * nb + t);
-    } else if constexpr (TYPE == SPIRAL_TYPE_Q8_0) {
-      task.load(PlanarQ8_0(w, n_rows, nb), n * nb * 2 + t);
-    } else {
-      task.load(PlanarQ6_K(w, n_rows, nb), n * nb + (t >> 2), static_cast<int>(t & 3));
-    }
-  }
-  __device__ __forceinline__ float compute(const uint8_t* lds, int64_t k) const {
-    if constexpr (TYPE == SPIRAL_TYPE_Q6_K) {
-      const int64_t kbase = (t >> 2) * 256 + ((t >> 1) & 1) * 128 + (t & 1) * 16;
-      return task.compute(lds, k, kbase);
-    } else {
-      return task.compute(lds, k, t);
-    }
-  }
+// ---- the kernel --------------------------------------------------------------
+
+template <int TYPE, int J>
+struct Unit {
+  typename Fmt<TYPE>::Payload p[J];
 };
 
-// Tasks of a row group (RPW rows) are numbered flat, f = r * T + t; lane l
-// takes f = l, l + 64, ... in chunks of UNROLL. All UNROLL payload loads of a
-// chunk are issued before the first is consumed; slots past the end load a
-// valid task of the group's first row and are discarded.
-template <int TYPE, int RPW, int UNROLL, bool F32_OUT>
-__global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const void* __restrict__ w, int64_t n_rows,
-                                                            int64_t k, const uint16_t* __restrict__ x,
-                                                            void* __restrict__ y) {
+// Requests the payload of pass `pass` of row `r`; tasks past the row's end
+// load task 0 (a valid address) and are masked out in compute_unit.
+template <int TYPE, int J, bool MASK>
+__device__ __forceinline__ void load_unit(Unit<TYPE, J>& U, const uint8_t* w, int64_t n_rows, int64_t k,
+                                          int64_t r, int pass, int T, int lane) {
+  using F = Fmt<TYPE>;
+  const typename F::Row R = F::row(w, n_rows, k, r);
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int t = pass * 64 * J + 64 * j + lane;
+    F::load(U.p[j], R, (!MASK || t < T) ? t : 0);
+  }
+}
+
+template <bool F32_OUT>
+__device__ __forceinline__ void store_y(void* y, int64_t r, float v) {
+  if constexpr (F32_OUT)
+    static_cast<float*>(y)[r] = v;
+  else
+    static_cast<__bf16*>(y)[r] = static_cast<__bf16>(v);
+}
+
+// XREG: the row fits one pass (T <= 64 J) and each lane keeps the x of its J
+// tasks in registers. MASK: some tasks of a pass fall past the row's end.
+// DEPTH: units whose payload is in flight at once (a ring of DEPTH buffers).
+template <int TYPE, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT>
+__global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
+                                                          int64_t k, const uint16_t* __restrict__ x,
+                                                          void* __restrict__ y) {
+  using F = Fmt<TYPE>;
   extern __shared__ __align__(16) uint8_t lds[];
-  stage_x<TYPE>(x, k, lds);
+  const int lane = threadIdx.x & 63;
+  const int64_t wave =
+      static_cast<int64_t>(blockIdx.x) * WAVES + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * WAVES;
+  const int64_t r0 = wave * n_rows / n_waves, r1 = (wave + 1) * n_rows / n_waves;
+  const int T = static_cast<int>(k / F::kTaskElems);
+  const int passes = XREG ? 1 : (T + 64 * J - 1) / (64 * J);
+  const int64_t units = (r1 - r0) * passes;
+
+  // Unit coordinates advance one pass at a time: (rl, pl) for loads, (rc, pc)
+  // for compute.
+  Unit<TYPE, J> buf[DEPTH];
+  int64_t rl = r0;
+  int pl = 0;
+  auto advance = [&](int64_t& r, int& pass) {
+    if (++pass == passes) { pass = 0; ++r; }
+  };
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    if (d < units) {
+      load_unit<TYPE, J, MASK>(buf[d], w, n_rows, k, rl, pl, T, lane);
+      advance(rl, pl);
+    }
+  }
+  F::stage(x, k, lds);
   __syncthreads();
 
-  using Tr = GemvTraits<TYPE>;
-  const int64_t nb = k / block_elems(TYPE);
-  const int64_t T = Tr::tasks_per_row(k);
-  const int64_t flat = RPW * T;
-  const int lane = threadIdx.x & 63;
-  const int64_t wave = blockIdx.x * kGemvWaves + (threadIdx.x >> 6);
-  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * kGemvWaves;
-  const int64_t n_groups = (n_rows + RPW - 1) / RPW;
-
-  for (int64_t g = wave; g < n_groups; g += n_waves) {
-    const int64_t row0 = g * RPW;
-    float acc[RPW];
+  typename F::X xr[XREG ? J : 1];
+  if constexpr (XREG) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-    for (int64_t f0 = lane; f0 < flat; f0 += 64 * UNROLL) {
-      Slot<TYPE> slot[UNROLL];
-      int rsel[UNROLL];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const int64_t f = f0 + 64 * u;
-        const int64_t r = f / T;
-        const bool valid = f < flat && row0 + r < n_rows;
-        rsel[u] = valid ? static_cast<int>(r) : -1;
-        const int64_t rr = valid ? r : 0;
-        slot[u].load(w, n_rows, nb, row0 + rr, valid ? f - r * T : 0);
-      }
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const float part = slot[u].compute(lds, k);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) acc[r] += (rsel[u] == r) ? part : 0.0f;
-      }
+    for (int j = 0; j < J; ++j) {
+      const int t = 64 * j + lane;
+      F::xload(xr[j], lds, T, (!MASK || t < T) ? t : 0);
     }
+  }
+
+  int64_t rc = r0;
+  int pc = 0;
+  float acc = 0.0f;
+  for (int64_t u0 = 0; u0 < units; u0 += DEPTH) {
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      const float v = wave_sum(acc[r]);
-      if (lane == 0 && row0 + r < n_rows) {
-        if constexpr (F32_OUT) {
-          static_cast<float*>(y)[row0 + r] = v;
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t u = u0 + d;
+      if (u >= units) break;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int t = pc * 64 * J + 64 * j + lane;
+        const bool ok = !MASK || t < T;
+        float part;
+        if constexpr (XREG) {
+          part = F::dot(buf[d].p[j], xr[j]);
         } else {
-          static_cast<__bf16*>(y)[row0 + r] = static_cast<__bf16>(v);
+          typename F::X xt;
+          F::xload(xt, lds, T, ok ? t : 0);
+          part = F::dot(buf[d].p[j], xt);
         }
+        acc += ok ? part : 0.0f;
+      }
+      if (pc == passes - 1) {
+        const float v = wave_sum(acc);
+        if (lane == 0) store_y<F32_OUT>(y, rc, v);
+        acc = 0.0f;
+      }
+      advance(rc, pc);
+      if (u + DEPTH < units) {
+        load_unit<TYPE, J, MASK>(buf[d], w, n_rows, k, rl, pl, T, lane);
+        advance(rl, pl);
       }
     }
   }
 }
 
-template <int TYPE, int RPW, int UNROLL>
-int launch_gemv(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
-                hipStream_t s) {
-  const int64_t lds = GemvTraits<TYPE>::lds_bytes(k);
-  const int per_cu = static_cast<int>(std::min<int64_t>(8, std::max<int64_t>(1, (160 * 1024) / lds)));
-  const int64_t groups = (n_rows + RPW - 1) / RPW;
-  const int64_t want = ceil_div(groups, kGemvWaves);
-  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(want, static_cast<int64_t>(device_cu_count()) * per_cu));
+// Resident workgroups per CU of a kernel at an LDS size (occupancy API,
+// cached per device, kernel and LDS size).
+int blocks_per_cu(const void* kernel, int threads, int64_t lds) {
+  struct Key {
+    int dev;
+    const void* kernel;
+    int64_t lds;
+    bool operator==(const Key& o) const { return dev == o.dev && kernel == o.kernel && lds == o.lds; }
+  };
+  struct Hash {
+    size_t operator()(const Key& k) const {
+      return std::hash<const void*>()(k.kernel) ^ (std::hash<int64_t>()(k.lds) * 31u) ^ static_cast<size_t>(k.dev);
+    }
+  };
+  static std::mutex mu;
+  static std::unordered_map<Key, int, Hash> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const Key key{dev, kernel, lds};
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, static_cast<size_t>(lds)) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  cache.emplace(key, n);
+  return n;
+}
+
+template <int TYPE, int J, int WAVES, int DEPTH, bool XREG, bool MASK>
+int launch_cfg(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  const int64_t lds = Fmt<TYPE>::lds_bytes(k);
+  const void* kern = y_type == SPIRAL_TYPE_F32
+                         ? reinterpret_cast<const void*>(gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, true>)
+                         : reinterpret_cast<const void*>(gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, false>);
+  const int64_t resident = static_cast<int64_t>(device_cu_count()) * blocks_per_cu(kern, 64 * WAVES, lds);
+  const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n_rows, WAVES), resident)));
+  const uint8_t* W = static_cast<const uint8_t*>(w);
   if (y_type == SPIRAL_TYPE_F32)
-    hipLaunchKernelGGL((gemv_kernel<TYPE, RPW, UNROLL, true>), dim3(blocks), dim3(kGemvThreads), lds, s, w, n_rows, k, x, y);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, true>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
+                       n_rows, k, x, y);
   else
-    hipLaunchKernelGGL((gemv_kernel<TYPE, RPW, UNROLL, false>), dim3(blocks), dim3(kGemvThreads), lds, s, w, n_rows, k, x, y);
+    hipLaunchKernelGGL((gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, false>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
+                       n_rows, k, x, y);
   return launch_status();
+}
+
+template <int TYPE, int J, int WAVES, int DEPTH>
+int launch_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  const int64_t T = k / Fmt<TYPE>::kTaskElems;
+  const bool xreg = T <= 64 * J, mask = T % (64 * J) != 0;
+  if (xreg)
+    return mask ? launch_cfg<TYPE, J, WAVES, DEPTH, true, true>(w, n_rows, k, x, y, y_type, s)
+                : launch_cfg<TYPE, J, WAVES, DEPTH, true, false>(w, n_rows, k, x, y, y_type, s);
+  return mask ? launch_cfg<TYPE, J, WAVES, DEPTH, false, true>(w, n_rows, k, x, y, y_type, s)
+              : launch_cfg<TYPE, J, WAVES, DEPTH, false, false>(w, n_rows, k, x, y, y_type, s);
+}
+
+// J = tasks per lane per unit, chosen so that rows of up to 64 J tasks keep x
+// in registers; two units in flight per wave (measured best on MI355X for
+// the 4096x14336 Q6_K, 14336x4096 Q8_0 and 4096x4096 Q4_0 shapes). Q6_K keeps
+// x in LDS (64 bf16 per task) with J = 1.
+template <int TYPE>
+int launch_gemv(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  const int64_t T = k / Fmt<TYPE>::kTaskElems;
+  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<TYPE, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 64) return launch_j<TYPE, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 128) return launch_j<TYPE, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  return launch_j<TYPE, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
 }
 
 }  // namespace
 
 // Largest k the LDS-staged GEMV accepts (64 KiB of staged x).
-int64_t gemv_max_k(int type) {
-  int64_t k = 0;
-  const int be = block_elems(type);
-  if (be == 0) return 0;
-  for (int64_t c = be;; c += be) {
-    const int64_t lds = type == SPIRAL_TYPE_Q4_0   ? GemvTraits<SPIRAL_TYPE_Q4_0>::lds_bytes(c)
-                        : type == SPIRAL_TYPE_Q8_0 ? GemvTraits<SPIRAL_TYPE_Q8_0>::lds_bytes(c)
-                                                   : GemvTraits<SPIRAL_TYPE_Q6_K>::lds_bytes(c);
-    if (lds > 64 * 1024) break;
-    k = c;
-  }
-  return k;
+template <int TYPE>
+int64_t max_k_of() {
+  using F = Fmt<TYPE>;
+  const int64_t per_task = F::lds_bytes(64 * F::kTaskElems) / 64;
+  return (kMaxLds / per_task / 64) * 64 * F::kTaskElems;
 }
 
-// y[n] = sum_k W[n][k] x[k]; arguments validated by the caller.
+int64_t gemv_max_k(int type) {
+  switch (type) {
+    case SPIRAL_TYPE_Q4_0: return max_k_of<SPIRAL_TYPE_Q4_0>();
+    case SPIRAL_TYPE_Q8_0: return max_k_of<SPIRAL_TYPE_Q8_0>();
+    case SPIRAL_TYPE_Q6_K: return max_k_of<SPIRAL_TYPE_Q6_K>();
+    default: return 0;
+  }
+}
+
+// y[n] = sum_k W[n][k] x[k]; arguments validated by the caller (k <= gemv_max_k).
 int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
          hipStream_t s) {
   switch (type) {
-    case SPIRAL_TYPE_Q4_0: return launch_gemv<SPIRAL_TYPE_Q4_0, 2, 2>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_Q8_0: return launch_gemv<SPIRAL_TYPE_Q8_0, 1, 4>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_Q6_K: return launch_gemv<SPIRAL_TYPE_Q6_K, 2, 2>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_Q4_0: return launch_gemv<SPIRAL_TYPE_Q4_0>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_Q8_0: return launch_gemv<SPIRAL_TYPE_Q8_0>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_Q6_K: return launch_gemv<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, y, y_type, s);
     default: return SPIRAL_ERR_TYPE;
   }
 }

@@ -2,9 +2,9 @@
 // quantized, expert-stacked weights).
 //
 // Two launches on the caller's stream:
-//  1. route_kernel (one workgroup): a stable counting sort of the
-//     (token, slot) pairs by expert id into per-expert lists in the caller's
-//     workspace; pairs with an out-of-range id get a zero output row.
+//  1. route_kernel (one workgroup): a counting sort of the (token, slot)
+//     pairs by expert id into per-expert lists in the caller's workspace;
+//     pairs with an out-of-range id get a zero output row.
 //  2. moe_kernel: workgroup (n-tile, expert) streams that expert's BN weight
 //     rows once and multiplies them against every token routed to it, 16
 //     tokens per MFMA row tile, up to 64 tokens per pass. Each expert's
@@ -21,57 +21,99 @@ namespace {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
-constexpr int kRouteThreads = 256;
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteChunk = 4096;  // experts counted per LDS pass
 constexpr int kMoeBN = 64, kMoeBK = 64, kMoeTok = 64;
 constexpr int kMoeLdsK = kMoeBK + 8;
 
 // Workspace: offsets[n_expert + 1] then list[n_pairs] (int32).
-__global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __restrict__ ids, int64_t n_pairs,
-                                                              int64_t n_expert, int32_t* __restrict__ offsets,
+//
+// One workgroup: per chunk of kRouteChunk experts, count the pairs of each
+// expert with LDS atomics, turn the counts into list offsets with a block
+// scan, then scatter each pair's index into its expert's list. The order
+// inside a list is arbitrary; each output row is computed on its own, so it
+// does not change any result. Pairs with an id outside [0, n_expert) get a
+// zero output row.
+__global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __restrict__ ids, int32_t n_pairs,
+                                                              int32_t n_expert, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ list, void* __restrict__ y,
                                                               int64_t n_rows, int y_f32) {
-  __shared__ int32_t s_counts[kRouteThreads];
-  __shared__ int32_t s_base;
-  if (threadIdx.x == 0) s_base = 0;
-  __syncthreads();
-  // Experts are processed kRouteThreads at a time; thread t owns expert
-  // e0 + t and scans all pairs in order, so each list keeps token order.
-  for (int64_t e0 = 0; e0 < n_expert; e0 += kRouteThreads) {
-    const int64_t e = e0 + threadIdx.x;
-    int32_t cnt = 0;
-    if (e < n_expert)
-      for (int64_t p = 0; p < n_pairs; ++p) cnt += (ids[p] == e);
-    s_counts[threadIdx.x] = cnt;
+  __shared__ int32_t s_cnt[kRouteChunk];
+  __shared__ int32_t s_wave[kRouteThreads / 64];
+  __shared__ int32_t s_bad[kRouteThreads];
+  __shared__ int32_t s_nbad;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  constexpr int kPer = kRouteChunk / kRouteThreads;
+  int32_t base = 0;
+  for (int32_t e0 = 0; e0 < n_expert; e0 += kRouteChunk) {
+    const int32_t ne = min(kRouteChunk, n_expert - e0);
+    for (int i = tid; i < kRouteChunk; i += kRouteThreads) s_cnt[i] = 0;
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int32_t run = s_base;
-      for (int t = 0; t < kRouteThreads && e0 + t < n_expert; ++t) {
-        const int32_t c = s_counts[t];
-        s_counts[t] = run;
-        offsets[e0 + t] = run;
-        run += c;
-      }
-      s_base = run;
+    for (int32_t p = tid; p < n_pairs; p += kRouteThreads) {
+      const int32_t e = ids[p] - e0;
+      if (e >= 0 && e < ne) atomicAdd(&s_cnt[e], 1);
     }
     __syncthreads();
-    if (e < n_expert) {
-      int32_t pos = s_counts[threadIdx.x];
-      for (int64_t p = 0; p < n_pairs; ++p)
-        if (ids[p] == e) list[pos++] = static_cast<int32_t>(p);
+    // Exclusive scan: thread t owns experts [kPer t, kPer t + kPer).
+    int32_t c[kPer], run = 0;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      c[i] = s_cnt[kPer * tid + i];
+      run += c[i];
     }
+    int32_t incl = run;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
+    }
+    if (lane == 63) s_wave[wv] = incl;
+    __syncthreads();
+    int32_t wbase = 0, total = 0;
+    for (int i = 0; i < kRouteThreads / 64; ++i) {
+      const int32_t v = s_wave[i];
+      wbase += i < wv ? v : 0;
+      total += v;
+    }
+    int32_t pos = base + wbase + incl - run;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = kPer * tid + i;
+      if (e < ne) offsets[e0 + e] = pos;
+      s_cnt[e] = pos;
+      pos += c[i];
+    }
+    __syncthreads();
+    for (int32_t p = tid; p < n_pairs; p += kRouteThreads) {
+      const int32_t e = ids[p] - e0;
+      if (e >= 0 && e < ne) list[atomicAdd(&s_cnt[e], 1)] = p;
+    }
+    base += total;
     __syncthreads();
   }
-  if (threadIdx.x == 0) offsets[n_expert] = s_base;
-  // Pairs routed nowhere produce a zero row.
-  for (int64_t p = 0; p < n_pairs; ++p) {
-    const int32_t e = ids[p];
-    if (e >= 0 && e < n_expert) continue;
-    for (int64_t c = threadIdx.x; c < n_rows; c += blockDim.x) {
-      if (y_f32)
-        static_cast<float*>(y)[p * n_rows + c] = 0.0f;
-      else
-        static_cast<uint16_t*>(y)[p * n_rows + c] = 0;
+  if (tid == 0) offsets[n_expert] = base;
+  // Pairs routed nowhere produce a zero row: collect them kRouteThreads at a
+  // time, then clear their rows with the whole workgroup.
+  for (int32_t p0 = 0; p0 < n_pairs; p0 += kRouteThreads) {
+    if (tid == 0) s_nbad = 0;
+    __syncthreads();
+    const int32_t p = p0 + tid;
+    if (p < n_pairs) {
+      const int32_t e = ids[p];
+      if (e < 0 || e >= n_expert) s_bad[atomicAdd(&s_nbad, 1)] = p;
     }
+    __syncthreads();
+    const int32_t nbad = s_nbad;
+    for (int32_t b = 0; b < nbad; ++b) {
+      const int64_t row = s_bad[b];
+      for (int64_t col = tid; col < n_rows; col += kRouteThreads) {
+        if (y_f32)
+          static_cast<float*>(y)[row * n_rows + col] = 0.0f;
+        else
+          static_cast<uint16_t*>(y)[row * n_rows + col] = 0;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -176,8 +218,8 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   int32_t* offsets = static_cast<int32_t*>(workspace);
   int32_t* list = offsets + n_expert + 1;
   const int f32 = y_type == SPIRAL_TYPE_F32;
-  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, n_pairs, n_expert, offsets, list, y,
-                     n_rows, f32);
+  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
+                     static_cast<int32_t>(n_expert), offsets, list, y, n_rows, f32);
   if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
   const dim3 grid(static_cast<unsigned>(ceil_div(n_rows, kMoeBN)), static_cast<unsigned>(n_expert));
   const uint8_t* W = static_cast<const uint8_t*>(w);
