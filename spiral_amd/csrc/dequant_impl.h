@@ -1,11 +1,20 @@
-// Exact dequantization of 8 consecutive elements of one planar row. Shared by
-// the standalone dequant / GET_ROWS kernels and the GEMM B-tile loaders, so
-// the fused products and the standalone dequant use one code path.
+// Exact dequantization helpers shared by the standalone dequant / GET_ROWS
+// kernels and the GEMM / MoE weight-tile loaders, so the fused products and
+// the standalone dequant cannot drift apart.
+//
+// Every element value is bf16_rne(exact product):
+//   Q4_0  (q - 8) * d, Q8_0 q * d, Q6_K d * sc * (q - 32)
+// (src/quants/q4_0/unpack.aie.h:31-46, src/quants/q8_0/unpack.aie.h:37-52,
+// src/quants/q6_k/unpack.aie.h:33-138). Each product is exact in fp32
+// (at most 24 significant bits), so one round-to-nearest-even conversion
+// (v_cvt_pk_bf16_f32) gives the reference's bits.
 #pragma once
 
 #include "common.h"
 
 namespace spiral {
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 // Eight dequantized values of group g (elements 8g..8g+7) of row n.
 template <int TYPE>
@@ -58,5 +67,188 @@ __device__ __forceinline__ void dequant8(const uint8_t* __restrict__ w, int64_t 
     }
   }
 }
+
+// ---- 16-element weight-tile pieces for the MFMA kernels -------------------
+//
+// A "piece" is 16 consecutive elements of one weight row starting at a
+// multiple of 16: its packed bytes are loaded into registers (Piece), then
+// dequantized to 16 bf16 (two uint4) and written to LDS. Splitting load and
+// dequant lets a kernel keep later tiles' loads in flight while it
+// multiplies the current one.
+//
+// Pieces are read with buffer loads: Piece::Addr fixes, per thread, the row
+// and the piece's place inside a 128-element k step (pl = 0..7), and a step
+// adds only scalar offsets. Offsets are 32-bit, so every plane of the
+// weight tensor must stay below 4 GiB (checked by the launcher).
+//
+// The values equal dequant8's. The one difference is the sign of a zero
+// weight (code 8 of Q4_0, 0 of Q8_0, 32 of Q6_K) under a negative scale: +0
+// here, -0 in dequant8. Zero weights contribute nothing to a product, so
+// the products are unaffected; the bit-exact dequant entry points use
+// dequant8.
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  // Third dword 0x00020000: raw (untyped) 32-bit accesses on gfx9-class GPUs.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+template <int TYPE>
+struct Piece;
+
+// Buffer resources over the planes of one planar weight tensor.
+struct Planes {
+  __amdgpu_buffer_rsrc_t a, b, c, d;
+};
+
+template <int TYPE>
+__device__ __forceinline__ Planes make_planes(const uint8_t* w, int64_t n_rows, int64_t nb) {
+  const int64_t tot = n_rows * nb;
+  Planes P;
+  if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
+    P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 16));
+    P.d = buffer_rsrc(w + tot * 16, static_cast<uint32_t>(tot * 2));
+    P.b = P.c = P.a;
+  } else if constexpr (TYPE == SPIRAL_TYPE_Q8_0) {
+    P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 32));
+    P.d = buffer_rsrc(w + tot * 32, static_cast<uint32_t>(tot * 2));
+    P.b = P.c = P.a;
+  } else {
+    P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 128));
+    P.b = buffer_rsrc(w + tot * 128, static_cast<uint32_t>(tot * 64));
+    P.c = buffer_rsrc(w + tot * 192, static_cast<uint32_t>(tot * 16));
+    P.d = buffer_rsrc(w + tot * 208, static_cast<uint32_t>(tot * 2));
+  }
+  return P;
+}
+
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bload1(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b8(r, voff, soff, 0);
+}
+
+// Q4_0: piece 2b + h of a row is nibble h of block b's 16 qs bytes.
+template <>
+struct Piece<SPIRAL_TYPE_Q4_0> {
+  uint4 q;
+  uint32_t d;
+  struct Addr {
+    uint32_t qs, d;
+    int hi;
+  };
+  // Row n, local piece pl of a 128-element step.
+  static __device__ __forceinline__ Addr addr(int64_t n, int64_t nb, int pl) {
+    const uint32_t b = static_cast<uint32_t>(n * nb) + (pl >> 1);
+    return Addr{b * 16u, b * 2u, pl & 1};
+  }
+  // Step starting at element k0 (a multiple of 128).
+  __device__ __forceinline__ void load(const Planes& P, const Addr& A, int64_t k0) {
+    const uint32_t kb = static_cast<uint32_t>(k0 >> 5);
+    q = bload16(P.a, A.qs, kb * 16u);
+    d = bload2(P.d, A.d, kb * 2u);
+  }
+  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
+  // fp16 (1024 + c) times d minus 1032 d is (c - 8) d, exact inside the FMA.
+  __device__ __forceinline__ void dequant(const Addr& A, uint4& o0, uint4& o1) const {
+    const float df = fp16_scale(d), off = -1032.0f * df;
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = (A.hi ? (w[i] >> 4) : w[i]) & 0x0F0F0F0Fu;
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), df, off), __builtin_fmaf(static_cast<float>(a.y), df, off));
+      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), df, off), __builtin_fmaf(static_cast<float>(b.y), df, off));
+    }
+    o0 = make_uint4(o[0], o[1], o[2], o[3]);
+    o1 = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+};
+
+// Q8_0: piece 2b + h of a row is qs[16h .. 16h + 15] of block b.
+template <>
+struct Piece<SPIRAL_TYPE_Q8_0> {
+  uint4 q;
+  uint32_t d;
+  struct Addr {
+    uint32_t qs, d;
+  };
+  static __device__ __forceinline__ Addr addr(int64_t n, int64_t nb, int pl) {
+    const uint32_t b = static_cast<uint32_t>(n * nb) + (pl >> 1);
+    return Addr{b * 32u + 16u * (pl & 1), b * 2u};
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& A, int64_t k0) {
+    const uint32_t kb = static_cast<uint32_t>(k0 >> 5);
+    q = bload16(P.a, A.qs, kb * 32u);
+    d = bload2(P.d, A.d, kb * 2u);
+  }
+  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
+  // (q ^ 0x80) is q + 128: fp16 (1024 + q + 128) times d minus 1152 d.
+  __device__ __forceinline__ void dequant(const Addr&, uint4& o0, uint4& o1) const {
+    const float df = fp16_scale(d), off = -1152.0f * df;
+    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u));
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), df, off), __builtin_fmaf(static_cast<float>(a.y), df, off));
+      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), df, off), __builtin_fmaf(static_cast<float>(b.y), df, off));
+    }
+    o0 = make_uint4(o[0], o[1], o[2], o[3]);
+    o1 = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+};
+
+// Q6_K: a 128-element step is half h = (k0 / 128) % 2 of super-block k0 / 256;
+// local piece pl covers elements 128 h + 32 j + l0 + i (j = pl / 2,
+// l0 = 16 (pl % 2), i < 16) with the single sub-scale sc[8 h + pl % 2 + 2 j].
+template <>
+struct Piece<SPIRAL_TYPE_Q6_K> {
+  uint4 lo, hb;
+  uint32_t ds_bits;  // fp16 d (low 16 bits) and the int8 sub-scale (bits 16..23)
+  struct Addr {
+    uint32_t ql, qh, sc, d;
+    int ls, hs;  // nibble shift (0 or 4) and 2-bit field shift (2 j)
+  };
+  static __device__ __forceinline__ Addr addr(int64_t n, int64_t nb, int pl) {
+    const uint32_t blk = static_cast<uint32_t>(n * nb);
+    const int j = pl >> 1, l0 = 16 * (pl & 1);
+    return Addr{blk * 128u + 32u * (j & 1) + l0, blk * 64u + l0, blk * 16u + (pl & 1) + 2 * j, blk * 2u,
+                (j >> 1) * 4, 2 * j};
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& A, int64_t k0) {
+    const uint32_t sb = static_cast<uint32_t>(k0 >> 8), h = static_cast<uint32_t>((k0 >> 7) & 1);
+    lo = bload16(P.a, A.ql, sb * 128u + 64u * h);
+    hb = bload16(P.b, A.qh, sb * 64u + 32u * h);
+    const uint32_t sc = bload1(P.c, A.sc, sb * 16u + 8u * h);
+    ds_bits = bload2(P.d, A.d, sb * 2u) | (sc << 16);
+  }
+  __device__ __forceinline__ void zero() { lo = hb = make_uint4(0u, 0u, 0u, 0u); ds_bits = 0u; }
+  // ds = d * sc is exact (<= 19 bits); code * ds - 32 ds is exact in the FMA
+  // and fits fp32 (<= 24 bits).
+  __device__ __forceinline__ void dequant(const Addr& A, uint4& o0, uint4& o1) const {
+    const float ds = fp16_scale(ds_bits & 0xffffu) * static_cast<float>(static_cast<int8_t>(ds_bits >> 16));
+    const float off = -32.0f * ds;
+    const uint32_t L[4] = {lo.x, lo.y, lo.z, lo.w}, H[4] = {hb.x, hb.y, hb.z, hb.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = ((L[i] >> A.ls) & 0x0F0F0F0Fu) | (((H[i] >> A.hs) & 0x03030303u) << 4);
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(c & 0xffu), ds, off),
+                             __builtin_fmaf(static_cast<float>((c >> 8) & 0xffu), ds, off));
+      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>((c >> 16) & 0xffu), ds, off),
+                                 __builtin_fmaf(static_cast<float>(c >> 24), ds, off));
+    }
+    o0 = make_uint4(o[0], o[1], o[2], o[3]);
+    o1 = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+};
 
 }  // namespace spiral
