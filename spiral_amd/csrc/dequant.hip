@@ -11,37 +11,42 @@
 //
 // Work item: one group of 8 consecutive output elements of one row, written
 // as one 16-byte store, so consecutive lanes store consecutive 16 bytes.
+// Grids larger than 2^32 - 1 workgroups, or rows longer than 2^32 - 1 groups,
+// are rejected with SPIRAL_ERR_SHAPE.
 #include "common.h"
 #include "dequant_impl.h"
 
 namespace spiral {
 namespace {
 
+// A workgroup covers 256 groups of 8 elements of one row; row and group
+// come from the workgroup index with one 32-bit scalar division, so no
+// thread divides.
 template <int TYPE>
 __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
-                                                      int64_t nb, int64_t groups_per_row,
+                                                      int64_t nb, uint32_t groups_per_row, uint32_t wg_per_row,
                                                       uint16_t* __restrict__ out, int64_t ld_out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n_rows * groups_per_row) return;
-  const int64_t n = i / groups_per_row, g = i % groups_per_row;
+  const uint32_t row = blockIdx.x / wg_per_row;
+  const uint32_t g = (blockIdx.x - row * wg_per_row) * 256 + threadIdx.x;
+  if (g >= groups_per_row) return;
   float v[8];
-  dequant8<TYPE>(w, n_rows, nb, n, g, v);
+  dequant8<TYPE>(w, n_rows, nb, row, g, v);
   uint4 o;
   o.x = pack_bf16x2(v[0], v[1]);
   o.y = pack_bf16x2(v[2], v[3]);
   o.z = pack_bf16x2(v[4], v[5]);
   o.w = pack_bf16x2(v[6], v[7]);
-  *reinterpret_cast<uint4*>(out + n * ld_out + 8 * g) = o;
+  *reinterpret_cast<uint4*>(out + row * ld_out + 8 * g) = o;
 }
 
 template <int TYPE, bool F32_OUT>
 __global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
-                                                       int64_t nb, int64_t groups_per_row,
-                                                       const int32_t* __restrict__ ids, int64_t n_ids,
-                                                       void* __restrict__ out, int64_t ld_out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n_ids * groups_per_row) return;
-  const int64_t r = i / groups_per_row, g = i % groups_per_row;
+                                                       int64_t nb, uint32_t groups_per_row, uint32_t wg_per_row,
+                                                       const int32_t* __restrict__ ids, void* __restrict__ out,
+                                                       int64_t ld_out) {
+  const uint32_t r = blockIdx.x / wg_per_row;
+  const uint32_t g = (blockIdx.x - r * wg_per_row) * 256 + threadIdx.x;
+  if (g >= groups_per_row) return;
   const int64_t n = ids[r];
   float v[8];
   if (n >= 0 && n < n_rows) {
@@ -80,16 +85,18 @@ int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k, uint
   if (!aligned16(w) || !aligned16(out) || ld_out % 8 != 0) return SPIRAL_ERR_ALIGN;
   int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
-  const int64_t nb = k / block_elems(type), gpr = k / 8;
-  const dim3 grid(static_cast<unsigned>(ceil_div(n_rows * gpr, 256)));
+  const int64_t nb = k / block_elems(type), gpr = k / 8, wpr = ceil_div(gpr, 256);
+  if (gpr > UINT32_MAX || n_rows > UINT32_MAX || n_rows * wpr > UINT32_MAX) return SPIRAL_ERR_SHAPE;
+  const dim3 grid(static_cast<unsigned>(n_rows * wpr));
+  const uint32_t g32 = static_cast<uint32_t>(gpr), w32 = static_cast<uint32_t>(wpr);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* W = static_cast<const uint8_t*>(w);
   if (type == SPIRAL_TYPE_Q4_0)
-    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q4_0>, grid, dim3(256), 0, s, W, n_rows, nb, gpr, out, ld_out);
+    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q4_0>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out);
   else if (type == SPIRAL_TYPE_Q8_0)
-    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q8_0>, grid, dim3(256), 0, s, W, n_rows, nb, gpr, out, ld_out);
+    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q8_0>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out);
   else
-    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q6_K>, grid, dim3(256), 0, s, W, n_rows, nb, gpr, out, ld_out);
+    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q6_K>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out);
   return launch_status();
 }
 
@@ -104,18 +111,20 @@ int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k, const in
   if (!aligned16(w) || !aligned16(out) || ld_out % 8 != 0) return SPIRAL_ERR_ALIGN;
   int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
-  const int64_t nb = k / block_elems(type), gpr = k / 8;
-  const dim3 grid(static_cast<unsigned>(ceil_div(n_ids * gpr, 256)));
+  const int64_t nb = k / block_elems(type), gpr = k / 8, wpr = ceil_div(gpr, 256);
+  if (gpr > UINT32_MAX || n_ids * wpr > UINT32_MAX) return SPIRAL_ERR_SHAPE;
+  const dim3 grid(static_cast<unsigned>(n_ids * wpr));
+  const uint32_t g32 = static_cast<uint32_t>(gpr), w32 = static_cast<uint32_t>(wpr);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* W = static_cast<const uint8_t*>(w);
 #define SPIRAL_GET_ROWS(T)                                                                      \
   do {                                                                                          \
     if (out_type == SPIRAL_TYPE_F32)                                                            \
-      hipLaunchKernelGGL((get_rows_kernel<T, true>), grid, dim3(256), 0, s, W, n_rows, nb, gpr, \
-                         ids, n_ids, out, ld_out);                                              \
+      hipLaunchKernelGGL((get_rows_kernel<T, true>), grid, dim3(256), 0, s, W, n_rows, nb, g32, \
+                         w32, ids, out, ld_out);                                                \
     else                                                                                        \
       hipLaunchKernelGGL((get_rows_kernel<T, false>), grid, dim3(256), 0, s, W, n_rows, nb,     \
-                         gpr, ids, n_ids, out, ld_out);                                         \
+                         g32, w32, ids, out, ld_out);                                           \
   } while (0)
   if (type == SPIRAL_TYPE_Q4_0) SPIRAL_GET_ROWS(SPIRAL_TYPE_Q4_0);
   else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_GET_ROWS(SPIRAL_TYPE_Q8_0);
