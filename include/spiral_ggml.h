@@ -1,0 +1,156 @@
+/*
+ * spiral_ggml.h -- a ggml-backend-shaped C surface over libspiral_quants.so:
+ * buffer type / buffer / tensor upload, supports_op and graph_compute for
+ * MUL_MAT, GET_ROWS and MUL_MAT_ID with quantized (Q4_0 / Q8_0 / Q6_K) src0,
+ * on one HIP device.
+ *
+ * The reference names this surface but does not contain it: its README says
+ * the NPU backend "will live in a llama.cpp fork" (README.md:11-14) and its
+ * repack header is meant to be compiled into that loader
+ * (src/quants/common/repack.h:5-7). ggml itself is not vendored. The types
+ * below therefore mirror the public ggml-backend interface field for field
+ * (ggml_tensor's type / buffer / ne / nb / op / src / data / name, ggml_cgraph's
+ * n_nodes / nodes, ggml_backend_buffer_i's alloc / free / get_base /
+ * init_tensor / set_tensor / get_tensor / memset_tensor / clear,
+ * ggml_backend_i's graph_compute / synchronize, ggml_backend_device_i's
+ * supports_op) without being ABI-identical to any ggml release: a llama.cpp
+ * backend shim copies its ggml_tensor fields into spiral_tensor one to one
+ * (the op ids differ between ggml releases and are mapped by that shim).
+ *
+ * Quantized tensors are stored on the device in the library's planar layout
+ * (see spiral_quants.h section 3): set_tensor converts canonical GGUF bytes
+ * to planar, get_tensor converts back, so the buffer looks canonical from
+ * the host. Byte counts are unchanged (the planar layout is a permutation of
+ * each 2-D matrix's bytes), so ggml's allocator sizes still hold.
+ *
+ * Errors: functions return spiral_status codes (spiral_quants.h); nothing
+ * aborts the process. Not thread-safe per backend or buffer (as ggml).
+ */
+#ifndef SPIRAL_GGML_H
+#define SPIRAL_GGML_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "spiral_quants.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SPIRAL_MAX_DIMS 4
+#define SPIRAL_MAX_SRC 10
+#define SPIRAL_MAX_NAME 64
+
+/* Operations this backend knows (the subset of ggml_op it takes part in).
+ * NONE / VIEW / RESHAPE / PERMUTE / TRANSPOSE are no-ops at compute time, as
+ * in every ggml backend. */
+typedef enum spiral_op {
+  SPIRAL_OP_NONE = 0,
+  SPIRAL_OP_GET_ROWS = 1,
+  SPIRAL_OP_MUL_MAT = 2,
+  SPIRAL_OP_MUL_MAT_ID = 3,
+  SPIRAL_OP_VIEW = 4,
+  SPIRAL_OP_RESHAPE = 5,
+  SPIRAL_OP_PERMUTE = 6,
+  SPIRAL_OP_TRANSPOSE = 7
+} spiral_op;
+
+typedef struct spiral_buffer spiral_buffer;   /* device memory block (opaque) */
+typedef struct spiral_backend spiral_backend; /* one device + stream (opaque) */
+
+/* ggml_tensor's fields that a backend reads: type (SPIRAL_TYPE_*, the ggml
+ * type ids), ne (elements per dimension, ne[0] innermost), nb (byte strides),
+ * op and src (the node's inputs), data (device address inside `buffer`). */
+typedef struct spiral_tensor {
+  int32_t type;
+  spiral_buffer* buffer;
+  int64_t ne[SPIRAL_MAX_DIMS];
+  size_t nb[SPIRAL_MAX_DIMS];
+  int32_t op;
+  struct spiral_tensor* src[SPIRAL_MAX_SRC];
+  void* data;
+  char name[SPIRAL_MAX_NAME];
+} spiral_tensor;
+
+typedef struct spiral_cgraph {
+  int32_t n_nodes;
+  spiral_tensor** nodes;
+} spiral_cgraph;
+
+/* ---- buffer type (ggml_backend_buffer_type_i) ------------------------- */
+
+const char* spiral_buft_name(void);
+/* Alignment of tensor data inside a buffer (ggml get_alignment). */
+size_t spiral_buft_alignment(void);
+/* Largest single buffer (ggml get_max_size). */
+size_t spiral_buft_max_size(void);
+/* Bytes a tensor occupies (ggml get_alloc_size): ggml_nbytes, unchanged by
+ * the planar layout. 0 for an unsupported tensor. */
+size_t spiral_buft_alloc_size(const spiral_tensor* t);
+/* Allocates `size` bytes of device memory on the current device
+ * (ggml alloc_buffer). Returns NULL when size is 0 or allocation fails. */
+spiral_buffer* spiral_buft_alloc_buffer(size_t size);
+
+/* ---- buffer (ggml_backend_buffer_i) ------------------------------------ */
+
+void spiral_buffer_free(spiral_buffer* buf);
+void* spiral_buffer_get_base(const spiral_buffer* buf);
+size_t spiral_buffer_get_size(const spiral_buffer* buf);
+/* Checks that the tensor lies inside the buffer, is contiguous in its
+ * innermost dimension and, when quantized, has whole rows of blocks and
+ * contiguous 2-D matrices (nb[1] == row bytes, nb[2] == ne[1] * nb[1],
+ * nb[3] == ne[2] * nb[2]). Sets t->buffer (ggml init_tensor). */
+int spiral_buffer_init_tensor(spiral_buffer* buf, spiral_tensor* t);
+/* Host -> tensor bytes [offset, offset + size) in canonical (GGUF) byte order
+ * (ggml set_tensor). Quantized tensors are converted to planar on the device;
+ * any byte range is accepted. Synchronous. */
+int spiral_buffer_set_tensor(spiral_buffer* buf, spiral_tensor* t, const void* data, size_t offset, size_t size);
+/* Tensor bytes [offset, offset + size) -> host, in canonical byte order
+ * (ggml get_tensor). Synchronous. */
+int spiral_buffer_get_tensor(spiral_buffer* buf, const spiral_tensor* t, void* data, size_t offset, size_t size);
+/* Sets tensor bytes [offset, offset + size) to `value` (ggml memset_tensor).
+ * A constant byte pattern is the same in both layouts. */
+int spiral_buffer_memset_tensor(spiral_buffer* buf, spiral_tensor* t, uint8_t value, size_t offset, size_t size);
+/* Sets the whole buffer to `value` (ggml clear). */
+int spiral_buffer_clear(spiral_buffer* buf, uint8_t value);
+
+/* ---- device (ggml_backend_device_i) -------------------------------------- */
+
+/* 1 when graph_compute can run node `op` (ggml supports_op); pure host
+ * logic, no device needed:
+ *   MUL_MAT     src0 Q4_0/Q8_0/Q6_K in a spiral buffer (2-D matrices, planar,
+ *               ne[2], ne[3] dividing src1's), src1 F32 or BF16 with
+ *               contiguous rows, dst F32 [ne0 = src0 ne1, ne1 = src1 ne1, ...];
+ *   GET_ROWS    src0 quantized, src1 I32 [n_rows_out, ne02, ne03], dst F32 or
+ *               BF16 with contiguous rows;
+ *   MUL_MAT_ID  src0 quantized [k, n, n_expert], src1 F32/BF16
+ *               [k, x_slots (1 or top_k), n_tokens], src2 I32 [top_k,
+ *               n_tokens], dst F32 [n, top_k, n_tokens], all contiguous;
+ *   NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE.
+ * Row lengths must be multiples of the type's block (32, Q6_K 256). */
+int spiral_supports_op(const spiral_tensor* op);
+
+/* ---- backend (ggml_backend_i) -------------------------------------------- */
+
+/* Binds HIP device `device` and creates the backend's stream (default
+ * priority). NULL when the device does not exist. */
+spiral_backend* spiral_backend_init(int device);
+void spiral_backend_free(spiral_backend* be);
+const char* spiral_backend_name(const spiral_backend* be);
+/* The backend's hipStream_t (for callers that interleave their own work). */
+void* spiral_backend_stream(const spiral_backend* be);
+/* Runs the graph's nodes in order on the backend's stream (ggml
+ * graph_compute). Fails with SPIRAL_ERR_TYPE, before launching anything, if
+ * a node is not supported; device scratch (bf16 copies of F32 activations,
+ * MUL_MAT_ID routing lists) is owned by the backend and grows on demand.
+ * Asynchronous: returns when the work is queued. */
+int spiral_backend_graph_compute(spiral_backend* be, const spiral_cgraph* graph);
+/* Waits for the backend's stream (ggml synchronize). */
+int spiral_backend_synchronize(spiral_backend* be);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPIRAL_GGML_H */

@@ -1,0 +1,261 @@
+"""The ggml-backend-shaped surface (include/spiral_ggml.h), tested the way
+ggml's test-backend-ops tests a backend: build a node, run it through
+graph_compute, compare with a CPU reference (here the oracle).
+
+CPU tests: tensor sizes, supports_op's refusals, and that nothing pretends to
+work without a device. GPU tests: canonical-bytes set/get round trips through
+the planar device layout (whole matrices and arbitrary byte ranges), and
+MUL_MAT / GET_ROWS / MUL_MAT_ID nodes against the oracle.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from spiral_amd import ggml, synth
+from spiral_amd._lib import STATUS
+
+REL_TOL = 1e-2         # GEMV path (block-scaled sums)
+REL_TOL_EXACT_W = 1e-3  # MFMA paths (exact bf16 weights), F32 output
+
+
+def rel_err(y, ref):
+    y = np.asarray(y, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    rms = np.sqrt(np.mean(ref * ref))
+    return float(np.max(np.abs(y - ref) / np.maximum(np.abs(ref), rms)))
+
+
+def f32_of_bf16(bits):
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- CPU ----------------------------------------------------------------------
+
+def test_alloc_size_matches_ggml_nbytes(spiral_lib):
+    assert ggml.nbytes(ggml.new_tensor(ggml.TYPE_Q4_0, [4096, 4096])) == 9_437_184
+    assert ggml.nbytes(ggml.new_tensor(ggml.TYPE_Q8_0, [4096, 14336])) == 62_390_272
+    assert ggml.nbytes(ggml.new_tensor(ggml.TYPE_Q6_K, [14336, 4096])) == 48_168_960
+    assert ggml.nbytes(ggml.new_tensor(ggml.TYPE_Q4_0, [2048, 1536, 128])) == 128 * 1_769_472
+    assert ggml.nbytes(ggml.new_tensor(ggml.TYPE_F32, [4, 3, 2])) == 96
+    assert ggml.nbytes(ggml.new_tensor(ggml.TYPE_BF16, [8, 5])) == 80
+    # a transposed F32 view: ggml_nbytes counts the span it reaches
+    t = ggml.new_tensor(ggml.TYPE_F32, [3, 4])
+    t.ne[0], t.ne[1] = 4, 3
+    t.nb[0], t.nb[1] = 12, 4
+    assert ggml.nbytes(t) == 4 + 3 * 12 + 2 * 4
+    with pytest.raises(ValueError):
+        ggml.new_tensor(ggml.TYPE_Q6_K, [100, 2])
+
+
+def test_buffer_type_properties(spiral_lib):
+    L = ggml._lib()
+    assert L.spiral_buft_name() == b"SPIRAL_MI355X"
+    assert L.spiral_buft_alignment() == 256
+    assert L.spiral_buft_max_size() > 1 << 40
+
+
+def test_supports_op_refusals(spiral_lib):
+    a = ggml.new_tensor(ggml.TYPE_Q4_0, [256, 64])
+    b = ggml.new_tensor(ggml.TYPE_F32, [256, 4])
+    # src0 has no buffer: not this backend's weights
+    assert not ggml.supports_op(ggml.mul_mat(a, b))
+    # dense src0, integer activations, shape mismatch, unknown op
+    assert not ggml.supports_op(ggml.mul_mat(ggml.new_tensor(ggml.TYPE_F32, [256, 64]), b))
+    assert not ggml.supports_op(ggml.mul_mat(a, ggml.new_tensor(ggml.TYPE_I32, [256, 4])))
+    assert not ggml.supports_op(ggml.mul_mat(a, ggml.new_tensor(ggml.TYPE_F32, [128, 4])))
+    odd = ggml.new_tensor(ggml.TYPE_F32, [1, 1])
+    odd.op = 99
+    assert not ggml.supports_op(odd)
+    for op in (ggml.OP_NONE, ggml.OP_VIEW, ggml.OP_RESHAPE, ggml.OP_PERMUTE, ggml.OP_TRANSPOSE):
+        v = ggml.new_tensor(ggml.TYPE_F32, [4])
+        v.op = op
+        assert ggml.supports_op(v)
+
+
+def test_no_device_means_no_backend(spiral_lib):
+    if spiral_lib.spiral_device_count() > 0:
+        pytest.skip("a HIP device is visible")
+    L = ggml._lib()
+    assert not L.spiral_buft_alloc_buffer(1 << 20)
+    with pytest.raises(RuntimeError):
+        ggml.Backend(0)
+    assert L.spiral_backend_graph_compute(None, None) == 3  # SPIRAL_ERR_NULL
+    assert L.spiral_buffer_set_tensor(None, None, None, 0, 0) == 3
+
+
+# ---- GPU ----------------------------------------------------------------------
+
+def weights(qtype, k, n, n_mat, seed):
+    """Canonical bytes of n_mat stacked [n][k] matrices."""
+    return np.concatenate([synth.make_weights(qtype, n, k, seed + i) for i in range(n_mat)])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+def test_set_get_round_trip_any_range(cuda, qtype):
+    k, n, n_mat = O.BLOCK_ELEMS[qtype] * 3, 8, 3   # 24 blocks: each matrix a multiple of 16 bytes
+    raw = weights(qtype, k, n, n_mat, 5)
+    buf = ggml.Buffer(1 << 20)
+    t = buf.alloc(ggml.new_tensor(qtype, [k, n, n_mat]))
+    assert ggml.nbytes(t) == raw.size
+    buf.set(t, raw.tobytes())                     # whole matrices
+    assert buf.get(t) == raw.tobytes()
+    buf.memset(t, 0)
+    assert buf.get(t) == bytes(raw.size)
+    rng = np.random.default_rng(qtype)
+    cuts = np.sort(rng.choice(np.arange(1, raw.size), 5, replace=False))
+    for lo, hi in zip([0, *cuts], [*cuts, raw.size]):  # arbitrary byte ranges
+        buf.set(t, raw[lo:hi].tobytes(), offset=int(lo))
+    assert buf.get(t) == raw.tobytes()
+    lo, hi = int(cuts[1]), int(cuts[3])
+    assert buf.get(t, size=hi - lo, offset=lo) == raw[lo:hi].tobytes()
+    buf.memset(t, 0x5A, offset=3, size=11)
+    want = raw.copy()
+    want[3:14] = 0x5A
+    assert buf.get(t) == want.tobytes()
+    # the device copy is planar: GET_ROWS reads it as the oracle reads canonical bytes
+    buf.set(t, raw.tobytes())
+    ids = buf.alloc(ggml.new_tensor(ggml.TYPE_I32, [4, n_mat]))
+    idv = np.array([[0, 7, 3, 3], [1, 2, 5, 0], [6, 6, 0, 4]], dtype=np.int32)
+    buf.set(ids, idv.tobytes())
+    out = buf.alloc(ggml.get_rows(t, ids, ggml.TYPE_BF16))
+    be = ggml.Backend(0)
+    assert be.graph_compute([out]) == 0
+    be.synchronize()
+    got = np.frombuffer(buf.get(out), dtype=np.uint16).reshape(n_mat, 4, k)
+    mat = raw.size // n_mat
+    for i in range(n_mat):
+        assert np.array_equal(got[i], O.get_rows(qtype, raw[i * mat:(i + 1) * mat], n, k, idv[i]))
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
+def test_stacks_must_be_16_byte_matrices(cuda):
+    """A stack whose matrices are not whole 16-byte multiples cannot hold the
+    per-matrix planar layout and is refused; a single such matrix is fine."""
+    buf = ggml.Buffer(1 << 20)
+    one = buf.alloc(ggml.new_tensor(O.Q4_0, [96, 7]))  # 378 bytes
+    raw = synth.make_weights(O.Q4_0, 7, 96, 9)
+    buf.set(one, raw.tobytes())
+    assert buf.get(one) == raw.tobytes()
+    stack = ggml.new_tensor(O.Q4_0, [96, 7, 2])
+    stack.data = buf.base + 4096
+    assert STATUS[ggml._lib().spiral_buffer_init_tensor(buf.ptr, ctypes.byref(stack))] == "SPIRAL_ERR_SHAPE"
+    buf.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+@pytest.mark.parametrize("act", [ggml.TYPE_F32, ggml.TYPE_BF16])
+@pytest.mark.parametrize("m", [1, 6, 40])
+def test_mul_mat_node(cuda, qtype, act, m):
+    k, n = O.BLOCK_ELEMS[qtype] * 4, 80
+    raw = synth.make_weights(qtype, n, k, 11 + m)
+    rng = np.random.default_rng(m)
+    xf = rng.standard_normal((m, k), dtype=np.float32)
+    xb = synth.bf16_bits(xf)
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, n]))
+    buf.set(a, raw.tobytes())
+    b = buf.alloc(ggml.new_tensor(act, [k, m]))
+    buf.set(b, (xf if act == ggml.TYPE_F32 else xb).tobytes())
+    node = buf.alloc(ggml.mul_mat(a, b))
+    assert ggml.supports_op(node)
+    be = ggml.Backend(0)
+    assert be.graph_compute([node]) == 0
+    be.synchronize()
+    y = np.frombuffer(buf.get(node), dtype=np.float32).reshape(m, n)
+    ref = O.matmul_f64(O.dequant(qtype, raw, n, k), xb)   # F32 activations are rounded to bf16
+    assert rel_err(y, ref) <= (REL_TOL if m == 1 else REL_TOL_EXACT_W)
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
+def test_mul_mat_broadcast_batches(cuda):
+    """src0 [k, n, 2, 1] against src1 [k, m, 4, 3]: batch (i2, i3) uses
+    src0 matrix i2 / 2 (ggml's broadcast rule)."""
+    qtype, k, n, m = O.Q8_0, 256, 48, 3
+    raws = [synth.make_weights(qtype, n, k, 40 + i) for i in range(2)]
+    rng = np.random.default_rng(3)
+    xf = rng.standard_normal((3, 4, m, k), dtype=np.float32)
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, n, 2, 1]))
+    buf.set(a, np.concatenate(raws).tobytes())
+    b = buf.alloc(ggml.new_tensor(ggml.TYPE_F32, [k, m, 4, 3]))
+    buf.set(b, xf.tobytes())
+    node = buf.alloc(ggml.mul_mat(a, b))
+    be = ggml.Backend(0)
+    assert be.graph_compute([node]) == 0
+    be.synchronize()
+    y = np.frombuffer(buf.get(node), dtype=np.float32).reshape(3, 4, m, n)
+    for i3 in range(3):
+        for i2 in range(4):
+            ref = O.matmul_f64(O.dequant(qtype, raws[i2 // 2], n, k), synth.bf16_bits(xf[i3, i2]))
+            assert rel_err(y[i3, i2], ref) <= REL_TOL_EXACT_W
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q6_K])
+def test_mul_mat_id_node(cuda, qtype):
+    k, n, n_expert, top_k, n_tokens = O.BLOCK_ELEMS[qtype] * 2, 64, 6, 2, 10
+    raws = [synth.make_weights(qtype, n, k, 60 + e) for e in range(n_expert)]
+    rng = np.random.default_rng(8)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    xf = rng.standard_normal((n_tokens, 1, k), dtype=np.float32)
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, n, n_expert]))
+    buf.set(a, np.concatenate(raws).tobytes())
+    b = buf.alloc(ggml.new_tensor(ggml.TYPE_F32, [k, 1, n_tokens]))
+    buf.set(b, xf.tobytes())
+    it = buf.alloc(ggml.new_tensor(ggml.TYPE_I32, [top_k, n_tokens]))
+    buf.set(it, ids.tobytes())
+    node = buf.alloc(ggml.mul_mat_id(a, b, it))
+    assert ggml.supports_op(node)
+    be = ggml.Backend(0)
+    assert be.graph_compute([node]) == 0
+    be.synchronize()
+    y = np.frombuffer(buf.get(node), dtype=np.float32).reshape(n_tokens, top_k, n)
+    xb = synth.bf16_bits(xf[:, 0])
+    for t in range(n_tokens):
+        for s in range(top_k):
+            ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], n, k), xb[t][None])[0]
+            assert rel_err(y[t, s], ref) <= REL_TOL_EXACT_W
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
+def test_graph_of_several_nodes_and_refusal(cuda):
+    qtype, k, n = O.Q4_0, 128, 32
+    raw = synth.make_weights(qtype, n, k, 70)
+    buf = ggml.Buffer(1 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, n]))
+    buf.set(a, raw.tobytes())
+    ids = buf.alloc(ggml.new_tensor(ggml.TYPE_I32, [3]))
+    buf.set(ids, np.array([5, 0, 31], dtype=np.int32).tobytes())
+    emb = buf.alloc(ggml.get_rows(a, ids))                 # [k, 3] F32
+    view = ggml.new_tensor(ggml.TYPE_F32, [1])
+    view.op = ggml.OP_VIEW
+    prod = buf.alloc(ggml.mul_mat(a, emb))                  # [n, 3]
+    be = ggml.Backend(0)
+    assert be.graph_compute([emb, view, prod]) == 0
+    be.synchronize()
+    w = O.dequant(qtype, raw, n, k)
+    e = np.frombuffer(buf.get(emb), dtype=np.float32).reshape(3, k)
+    assert np.array_equal(e.view(np.uint32), w[[5, 0, 31]].astype(np.uint32) << 16)
+    y = np.frombuffer(buf.get(prod), dtype=np.float32).reshape(3, n)
+    assert rel_err(y, O.matmul_f64(w, w[[5, 0, 31]])) <= REL_TOL_EXACT_W
+    bad = ggml.mul_mat(a, ggml.new_tensor(ggml.TYPE_I32, [k, 2]))
+    before = buf.get(prod)
+    assert STATUS[be.graph_compute([prod, bad])] == "SPIRAL_ERR_TYPE"
+    be.synchronize()
+    assert buf.get(prod) == before  # refused before anything ran
+    be.free()
+    buf.free()
