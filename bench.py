@@ -1,6 +1,8 @@
 """Benchmark of the quantized-weight hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAME] [--no-cpu]
+    python bench.py --copy-calibration
+    python bench.py --write-traffic DIR   (DIR: rocprofv3 --pmc csv output, see below)
 
 Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
 x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
@@ -19,8 +21,15 @@ Measurement
     "ms_per_step" is its duration / K, "value" is K steps of algorithmic work
     over it (whole-job throughput, inputs resident in HBM), and
     "roofline.achieved" is the algorithmic bytes (or FLOPs) of one launch over
-    the mean step. "wall_ms_per_step" is the host clock around the same replay. "traffic" comes from rocprofv3 FETCH_SIZE / WRITE_SIZE counter
-    runs recorded in profiles/traffic.json when present.
+    the mean step. "wall_ms_per_step" is the host clock around the same replay.
+  - "roofline.traffic" is the HBM bytes one launch of the workload's kernel
+    moves, from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this
+    script, each scaled by the factor that makes a plain 256 MiB device copy
+    (--copy-calibration) read and write 256 MiB; the scaled figures are kept
+    in profiles/traffic.json (null when that file is absent). --write-traffic
+    DIR rebuilds that file from DIR/{bench,copy}_{FETCH,WRITE}_SIZE/
+    p_counter_collection.csv (rocprofv3 --pmc X --output-format csv -o p
+    over this script, and over this script with --copy-calibration).
   - "cpu_baseline": the CPU oracle's streaming dequantize-and-multiply over the
     same canonical Q8_0 tensor, on the host's cores, repeated for ~10 s.
 """
@@ -50,6 +59,10 @@ def parse():
     ap.add_argument("--only", default=None, help="run one workload (for profiling)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--write-traffic", metavar="DIR", default=None,
+                    help="rebuild profiles/traffic.json from rocprofv3 --pmc csv output in DIR")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run five 256 MiB device-to-device copies (known-size reference for HBM counters)")
     return ap.parse_args()
 
 
@@ -93,17 +106,90 @@ class Timer:
 
 
 def traffic_table():
+    """workload name -> scaled HBM bytes per launch, from profiles/traffic.json."""
     p = ROOT / "profiles" / "traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text())
-        except ValueError:
-            return {}
-    return {}
+    try:
+        kernels = json.loads(p.read_text()).get("kernels", {})
+    except (OSError, ValueError):
+        return {}
+    return {name: e.get("traffic_bytes") for name, e in kernels.items()}
+
+
+# workload -> (kernel-name fragments whose dispatches make one step, algorithmic
+# bytes of one step or None)
+TRAFFIC_KERNELS = {
+    "gemv_q8_0": (["gemv_kernel<8,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
+    "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
+    "gemv_q4_0": (["gemv_kernel<2,"], 4096 * 4096 // 32 * 18 + 4096 * 2 + 4096 * 2),
+    "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
+    "gemm_q4_0": (["gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
+    "moe_q4_0": (["moe_kernel<2,", "route_kernel"], None),
+}
+
+
+def write_traffic(d):
+    """Scaled HBM bytes per step from rocprofv3 FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch). Each counter is scaled so that the 256 MiB calibration copy
+    reads it as 256 MiB."""
+    import csv
+    from collections import defaultdict
+    d = Path(d)
+
+    def per_kernel(sub):
+        acc = defaultdict(list)
+        with open(d / sub / "p_counter_collection.csv") as f:
+            for r in csv.DictReader(f):
+                acc[r["Kernel_Name"].replace(" ", "")].append(float(r["Counter_Value"]))
+        return {k: sum(v) / len(v) for k, v in acc.items()}
+
+    def pick(table, frag):
+        hits = [v for k, v in table.items() if frag in k]
+        if len(hits) != 1:
+            raise SystemExit(f"{len(hits)} kernels match {frag!r}")
+        return hits[0]
+
+    bf, bw = per_kernel("bench_FETCH_SIZE"), per_kernel("bench_WRITE_SIZE")
+    cf, cw = per_kernel("copy_FETCH_SIZE"), per_kernel("copy_WRITE_SIZE")
+    kib = 256 * 1024
+    fs, ws = kib / pick(cf, "copyBuffer"), kib / pick(cw, "copyBuffer")
+    out = {"note": "HBM bytes per step: rocprofv3 FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled "
+                   "so that a 256 MiB device-to-device copy reads as 262144 KiB; MoE steps are two "
+                   "MUL_MAT_ID launches (route + grouped GEMM each)",
+           "copy_calibration": {"bytes": 256 << 20, "fetch_kb_raw": round(kib / fs, 1),
+                                "write_kb_raw": round(kib / ws, 1), "fetch_scale": round(fs, 4),
+                                "write_scale": round(ws, 4)},
+           "kernels": {}}
+    for name, (frags, alg) in TRAFFIC_KERNELS.items():
+        launches = 2 if name == "moe_q4_0" else 1
+        f = sum(pick(bf, fr) for fr in frags) * launches
+        w = sum(pick(bw, fr) for fr in frags) * launches
+        tb = (f * fs + w * ws) * 1024
+        e = {"kernels": frags, "launches_per_step": launches, "fetch_kb_raw": round(f, 1),
+             "write_kb_raw": round(w, 1), "traffic_bytes": int(round(tb))}
+        if alg:
+            e["algorithmic_bytes"] = alg
+            e["traffic_over_algorithmic"] = round(tb / alg, 3)
+        out["kernels"][name] = e
+    dst = ROOT / "profiles" / "traffic.json"
+    dst.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out, indent=1))
+
+
+def copy_calibration(torch):
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 5}))
 
 
 def main():
     args = parse()
+    if args.write_traffic:
+        write_traffic(args.write_traffic)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}))
@@ -115,6 +201,9 @@ def main():
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a HIP device")
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
     lib()  # fail loudly if the library is missing
     dev = torch.device("cuda:0")
     timer = Timer(torch)
@@ -273,10 +362,11 @@ def main():
         raise SystemExit(f"unknown workload {args.only}")
 
     traffic = traffic_table()
+    for name, r in results.items():
+        r["roofline"]["traffic"] = traffic.get(name)
     head_name = "gemv_q8_0" if "gemv_q8_0" in results else next(iter(results))
     head = results[head_name]
     roof = dict(head["roofline"])
-    roof["traffic"] = traffic.get(head_name)
 
     cpu = None
     if head_name == "gemv_q8_0" and not args.no_cpu:
