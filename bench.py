@@ -122,7 +122,7 @@ TRAFFIC_KERNELS = {
     "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
     "gemv_q4_0": (["gemv_kernel<2,"], 4096 * 4096 // 32 * 18 + 4096 * 2 + 4096 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
-    "gemm_q4_0": (["gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
+    "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
     "moe_q4_0": (["moe_kernel<2,", "route_kernel"], None),
 }
 
@@ -300,11 +300,13 @@ def main():
         _, ws = upload_planar(TYPE_Q4_0, n, k, 7, copies)
         xs = [x_dev(m, k, 8 + c)[1] for c in range(copies)]
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        gws = ops.mul_mat_workspace(TYPE_Q4_0, n, k, m, dev)
         flops = 2.0 * m * n * k
-        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y),
-                               steps, warmup)
+        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y,
+                                                   workspace=gws), steps, warmup)
         record("gemm_q4_0", wall, ev, flops, "TFLOP/s", MFMA_BF16_PEAK_TFS, "mfma",
-               {"workload": "Q4_0 prefill dequant-GEMM Y[512x4096] = X[512x4096] W[4096x4096]^T, bf16 MFMA, fp32 acc",
+               {"workload": "Q4_0 prefill dequant-GEMM Y[512x4096] = X[512x4096] W[4096x4096]^T, bf16 MFMA, fp32 acc "
+                            "(one step = X packing + GEMM kernel)",
                 "flops_per_launch": flops, "copies": copies})
         del ws, xs
 

@@ -151,10 +151,17 @@ int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k,
 /* ggml MUL_MAT with quantized src0: y[i][n] = sum_k x[i][k] * W[n][k] for
  * i < m, x bf16 rows of stride ldx elements, y (BF16 or F32) rows of stride ldy
  * elements. fp32 accumulation. m == 1 runs the streaming GEMV; larger m runs
- * the MFMA dequant-GEMM. */
+ * the MFMA dequant-GEMM, which first rewrites x into MFMA operand order in
+ * `workspace` (device memory, 16-byte aligned, caller-owned; at least
+ * spiral_mul_mat_workspace_bytes() bytes, which is 0 when the GEMV runs, in
+ * which case workspace may be NULL). A workspace must not be shared by calls
+ * in flight at the same time. */
+int64_t spiral_mul_mat_workspace_bytes(int type, int64_t n_rows, int64_t k,
+                                       int64_t m);
 int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k,
                    const uint16_t* x, int64_t ldx, int64_t m, void* y,
-                   int y_type, int64_t ldy, void* stream);
+                   int y_type, int64_t ldy, void* workspace,
+                   int64_t workspace_bytes, void* stream);
 
 /* ggml MUL_MAT_ID with quantized, expert-stacked src0: for token t < n_tokens
  * and slot s < top_k, y[t][s][:] = W[ids[t][s]] * x[t][s % x_slots][:].

@@ -47,7 +47,8 @@ SIGNATURES = {
     "spiral_from_planar": (_int, [_int, _p, _i64, _i64, _p, _i64, _p]),
     "spiral_dequant_bf16": (_int, [_int, _p, _i64, _i64, _p, _i64, _p]),
     "spiral_get_rows": (_int, [_int, _p, _i64, _i64, _p, _i64, _p, _int, _i64, _p]),
-    "spiral_mul_mat": (_int, [_int, _p, _i64, _i64, _p, _i64, _i64, _p, _int, _i64, _p]),
+    "spiral_mul_mat_workspace_bytes": (_i64, [_int, _i64, _i64, _i64]),
+    "spiral_mul_mat": (_int, [_int, _p, _i64, _i64, _p, _i64, _i64, _p, _int, _i64, _p, _i64, _p]),
     "spiral_mul_mat_id_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "spiral_mul_mat_id": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,
                                  _p, _i64, _p]),

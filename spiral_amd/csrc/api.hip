@@ -5,8 +5,9 @@ namespace spiral {
 int64_t gemv_max_k(int type);
 int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
          hipStream_t s);
+int64_t gemm_workspace_bytes(int64_t m, int64_t k);
 int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m,
-         void* y, int y_type, int64_t ldy, hipStream_t s);
+         void* y, int y_type, int64_t ldy, void* workspace, hipStream_t s);
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs);
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
@@ -17,8 +18,15 @@ using namespace spiral;
 
 extern "C" {
 
+int64_t spiral_mul_mat_workspace_bytes(int type, int64_t n_rows, int64_t k, int64_t m) {
+  if (!is_quant_type(type) || n_rows <= 0 || m <= 0 || k <= 0 || k % block_elems(type) != 0) return 0;
+  if (m == 1 && k <= gemv_max_k(type)) return 0;
+  return gemm_workspace_bytes(m, k);
+}
+
 int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx,
-                   int64_t m, void* y, int y_type, int64_t ldy, void* stream) {
+                   int64_t m, void* y, int y_type, int64_t ldy, void* workspace, int64_t workspace_bytes,
+                   void* stream) {
   if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
   if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
   if (w == nullptr || x == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
@@ -26,11 +34,17 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uin
   if (ldx < k || ldy < n_rows) return SPIRAL_ERR_SHAPE;
   if (!aligned16(w) || !aligned16(x) || ldx % 8 != 0) return SPIRAL_ERR_ALIGN;
   if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0) return SPIRAL_ERR_ALIGN;
+  const int64_t need = spiral_mul_mat_workspace_bytes(type, n_rows, k, m);
+  if (need > 0) {
+    if (workspace == nullptr) return SPIRAL_ERR_NULL;
+    if (workspace_bytes < need) return SPIRAL_ERR_CAPACITY;
+    if (!aligned16(workspace)) return SPIRAL_ERR_ALIGN;
+  }
   int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (m == 1 && k <= gemv_max_k(type)) return gemv(type, w, n_rows, k, x, y, y_type, s);
-  return gemm(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
+  if (need == 0) return gemv(type, w, n_rows, k, x, y, y_type, s);
+  return gemm(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, workspace, s);
 }
 
 int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens, int64_t top_k) {

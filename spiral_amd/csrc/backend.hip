@@ -174,9 +174,17 @@ size_t act_scratch(const spiral_tensor* b) {
   return align_up(static_cast<size_t>(b->ne[0] * b->ne[1] * b->ne[2] * b->ne[3]) * 2, kAlign);
 }
 
+// Workspace of one MUL_MAT product (the batch's matrices run one after
+// another on the backend's stream and share it).
+size_t mul_mat_workspace(const spiral_tensor* t) {
+  const spiral_tensor* a = t->src[0];
+  const int64_t n = spiral_mul_mat_workspace_bytes(a->type, a->ne[1], a->ne[0], t->src[1]->ne[1]);
+  return align_up(static_cast<size_t>(n > 0 ? n : 0), kAlign);
+}
+
 size_t node_scratch(const spiral_tensor* t) {
   switch (t->op) {
-    case SPIRAL_OP_MUL_MAT: return act_scratch(t->src[1]);
+    case SPIRAL_OP_MUL_MAT: return act_scratch(t->src[1]) + mul_mat_workspace(t);
     case SPIRAL_OP_MUL_MAT_ID: {
       const spiral_tensor* b = t->src[1];
       const spiral_tensor* ids = t->src[2];
@@ -232,13 +240,15 @@ int compute_mul_mat(spiral_backend* be, const spiral_tensor* t) {
   const uint16_t* xb = act_bf16(b, be->scratch, false, be->stream, ld1, ld2, ld3, rc);
   if (rc != SPIRAL_OK) return rc;
   const int64_t r2 = b->ne[2] / a->ne[2], r3 = b->ne[3] / a->ne[3];
+  uint8_t* ws = be->scratch + act_scratch(b);
+  const int64_t wsb = static_cast<int64_t>(mul_mat_workspace(t));
   for (int64_t i3 = 0; i3 < b->ne[3]; ++i3) {
     for (int64_t i2 = 0; i2 < b->ne[2]; ++i2) {
       const uint8_t* w = static_cast<const uint8_t*>(a->data) + (i2 / r2) * a->nb[2] + (i3 / r3) * a->nb[3];
       const uint16_t* x = xb + i2 * ld2 + i3 * ld3;
       uint8_t* y = static_cast<uint8_t*>(t->data) + i2 * t->nb[2] + i3 * t->nb[3];
       rc = spiral_mul_mat(a->type, w, a->ne[1], a->ne[0], x, ld1, b->ne[1], y, SPIRAL_TYPE_F32,
-                          static_cast<int64_t>(t->nb[1] / 4), be->stream);
+                          static_cast<int64_t>(t->nb[1] / 4), wsb > 0 ? ws : nullptr, wsb, be->stream);
       if (rc != SPIRAL_OK) return rc;
     }
   }

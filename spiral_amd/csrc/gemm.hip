@@ -7,24 +7,33 @@
 // and multiplied against bf16 inputs with fp32 accumulation, so each product
 // term equals the reference's; only the fp32 summation order differs.
 //
-// Tiling (gfx950, wave64, v_mfma_f32_16x16x32_bf16, 16 cycles each):
-//  - One workgroup per 128 (m) x 64 (n) tile of Y; m = 512, n = 4096 gives
-//    256 tiles, one per CU.
-//  - A k step is 128 wide. Its W tile (64 rows x 128 k) is dequantized once
-//    per workgroup into LDS (double-buffered, one barrier per step): each of
-//    the 512 threads turns one 16-element piece.
-//  - 8 waves: wave w owns rows 32 (w % 4) .. + 31 (2 x 4 MFMA tiles) for the
-//    64-wide k half w / 4 of every step. Each SIMD thus runs two waves over
-//    the same rows and interleaves their instruction streams; the halves are
-//    summed through LDS at the end.
-//  - X goes straight from global memory into the MFMA A-operand layout with
-//    buffer loads (fixed per-lane offset + scalar per-step offset; each
-//    element of X is read by one wave of the workgroup, no LDS).
-//  - X fragments and packed weights are requested RING - 1 steps ahead in a
-//    register ring; step s + 1's weights are dequantized while step s's
-//    MFMAs run.
-//  - Workgroups are numbered so that each XCD (dispatch is round-robin over
-//    the 8 XCDs) gets a contiguous range of tiles that share X rows in its L2.
+// Two launches on the caller's stream:
+//  1. pack_x_kernel rewrites X into MFMA A-operand order in the caller's
+//     workspace: 1 KiB fragments Xp[m / 16][k / 32][lane][8], lane l holding
+//     row l % 16, k 8 (l / 16) .. + 7 of its 16 x 32 block. A wave then loads
+//     one fragment as 1 KiB of consecutive bytes (eight whole 128-byte lines),
+//     where loading it from X directly touches 16 rows x 64 bytes; on gfx950
+//     the latter pattern reaches about a third of the L2 -> CU throughput.
+//  2. gemm_kernel: one workgroup per 128 (m) x 64 (n) tile of Y (m = 512,
+//     n = 4096: 256 tiles, one per CU), 8 waves, k steps of 128.
+//      - The step's 64 x 128 weight tile is dequantized once per workgroup
+//        into LDS (each of the 512 threads turns one 16-element piece); LDS
+//        holds four such tiles, the one being read and the next three.
+//      - Wave (mw, q) = (w % 2, w / 2) owns rows 64 mw .. + 63 of the tile
+//        and the k-quarter q (32 wide, one MFMA depth) of every step: four
+//        X fragments (buffer loads from the packed workspace, no LDS) and
+//        four B fragments from LDS feed 16 v_mfma_f32_16x16x32_bf16. Each
+//        weight element is read from LDS by two waves, each X element by one.
+//      - Register rings keep X three steps and weights five steps ahead
+//        (Q6_K: one and three).
+//        Step s + 2's weights are dequantized while step s multiplies, so a
+//        barrier is needed only after every second step.
+//      - Scheduling fences keep each step's MFMAs, LDS reads, dequantization
+//        and loads together; without them the compiler hoists later steps'
+//        dequantization above the loads it waits for.
+//      - The four k-quarters are summed through LDS at the end.
+//  Workgroups are numbered so that each XCD (dispatch is round-robin over the
+//  8 XCDs) gets a contiguous range of tiles sharing X rows in its L2.
 #include <algorithm>
 
 #include "common.h"
@@ -39,7 +48,10 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 constexpr int kBM = 128, kBN = 64, kBK = 128, kThreads = 512;
 constexpr int kPitch = kBK + 8;  // LDS row pitch in bf16; the pad spreads rows over banks
 constexpr int kRing = 4;
+constexpr int kBTile = kBN * kPitch;                   // one weight tile in LDS (bf16)
+constexpr int kRedFloats = 2 * 4 * 3 * 16 * 64;        // k-quarter partials (floats)
 constexpr int64_t kMaxBufferBytes = int64_t(1) << 31;  // buffer offsets are 32-bit
+static_assert(4 * kBTile * 2 <= kRedFloats * 4, "weight tiles and partials share one LDS array");
 
 // Tile index for workgroup b of `grid`: consecutive workgroups go to
 // consecutive XCDs, so hand XCD x the tiles [x grid / 8, (x + 1) grid / 8).
@@ -48,22 +60,42 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t grid) {
   return (b % 8) * (grid / 8) + b / 8;
 }
 
+// Xp[mb][kk][lane][8] = X[16 mb + lane % 16][32 kk + 8 (lane / 16) + e];
+// rows past m are zero. Workgroup (mb, group of 16 kk): wave w writes the
+// four fragments kk = 16 g + 4 w .. + 3, four loads in flight per lane.
+__global__ void __launch_bounds__(256) pack_x_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t m,
+                                                     int64_t k, uint16_t* __restrict__ xp) {
+  const uint32_t kk_n = static_cast<uint32_t>(k >> 5);
+  const uint32_t groups = (kk_n + 15) >> 4;
+  const uint32_t mb = blockIdx.x / groups, kg = blockIdx.x - mb * groups;
+  const uint32_t lane = threadIdx.x & 63u, kk0 = 16 * kg + 4 * (threadIdx.x >> 6);
+  const int64_t r = 16 * static_cast<int64_t>(mb) + (lane & 15);
+  uint4 v[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    v[t] = make_uint4(0u, 0u, 0u, 0u);
+    if (r < m && kk0 + t < kk_n)
+      v[t] = *reinterpret_cast<const uint4*>(x + r * ldx + 32 * (kk0 + t) + 8 * (lane >> 4));
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    if (kk0 + t < kk_n)
+      *reinterpret_cast<uint4*>(xp + ((static_cast<int64_t>(mb) * kk_n + kk0 + t) * 64 + lane) * 8) = v[t];
+}
+
+// The four X fragments (m-blocks) of a wave for one k-quarter.
 struct AFrag {
-  uint4 v[2][2];  // [m16 block][k32 sub-step of the wave's half]
+  uint4 v[4];
 };
 
-// X fragments of a wave's 32 rows for its 64-wide half of a k step (k0 =
-// start of the half): lane l holds row (l % 16) of each 16-row block at
-// k = 8 (l / 16) .. + 7 of each 32-k sub-step. voff[i] is the lane's byte
-// offset of its row of block i (rows past m clamped to m - 1: their outputs
-// are never stored). Sub-steps at or past `nsub` are zero (the k tail).
-__device__ __forceinline__ void load_a(AFrag& a, __amdgpu_buffer_rsrc_t X, const uint32_t (&voff)[2], int64_t k0,
-                                       int nsub = 2) {
+// voff[i]: the lane's byte offset of m-block i's fragment row in the packed
+// workspace (blocks past m clamped: their outputs are never stored); the
+// k32 index k0 / 32 becomes the scalar offset.
+__device__ __forceinline__ void load_a(AFrag& a, __amdgpu_buffer_rsrc_t X, const uint32_t (&voff)[4], int64_t k0,
+                                       bool valid = true) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-      a.v[i][s] = s < nsub ? bload16(X, voff[i], static_cast<uint32_t>(k0 + 32 * s) * 2u) : make_uint4(0u, 0u, 0u, 0u);
+  for (int i = 0; i < 4; ++i)
+    a.v[i] = valid ? bload16(X, voff[i], static_cast<uint32_t>(k0 >> 5) * 1024u) : make_uint4(0u, 0u, 0u, 0u);
 }
 
 template <int TYPE>
@@ -76,185 +108,213 @@ __device__ __forceinline__ void store_b(const Piece<TYPE>& pc, const typename Pi
   *reinterpret_cast<uint4*>(dst + 8) = o1;
 }
 
-__device__ __forceinline__ bf16x8_t read_b(const uint16_t* bs, int j, int s, int lane) {
-  return *reinterpret_cast<const bf16x8_t*>(bs + (16 * j + (lane & 15)) * kPitch + 32 * s + 8 * (lane >> 4));
+// B operands of k-quarter q for the 64 columns: lane l takes column
+// 16 j + l % 16, k = 32 q + 8 (l / 16) .. + 7.
+struct BFrag {
+  bf16x8_t b[4];
+};
+
+__device__ __forceinline__ void read_bfrag(BFrag& f, const uint16_t* bs, int q, int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    f.b[j] = *reinterpret_cast<const bf16x8_t*>(bs + (16 * j + (lane & 15)) * kPitch + 32 * q + 8 * (lane >> 4));
 }
 
-// The wave's two K32 sub-steps (sub-steps 2 h and 2 h + 1 of the 128-wide
-// LDS tile) against all 64 columns.
-__device__ __forceinline__ void mfma_step(f32x4_t (&acc)[2][4], const AFrag& a, const uint16_t* bs, int h,
-                                          int lane) {
+__device__ __forceinline__ void mfma_step(f32x4_t (&acc)[4][4], const AFrag& a, const BFrag& b) {
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    bf16x8_t b[4];
+  for (int i = 0; i < 4; ++i) {
+    const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a.v[i]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = read_b(bs, j, 2 * h + s, lane);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a.v[i][s]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b[j], acc[i][j], 0, 0, 0);
-    }
+    for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, b.b[j], acc[i][j], 0, 0, 0);
   }
 }
 
-template <int TYPE, int RING>
+// Register rings: kARing<TYPE> X slots loaded kARing - 1 steps ahead and
+// kWRing<TYPE> weight-piece slots loaded kWRing + 1 steps ahead. Q6_K
+// pieces take twice the registers of the others, so its rings are shorter.
+template <int TYPE>
+constexpr int kARing = TYPE == SPIRAL_TYPE_Q6_K ? 2 : 4;
+template <int TYPE>
+constexpr int kWRing = TYPE == SPIRAL_TYPE_Q6_K ? 2 : 4;
+
+template <int TYPE>
 struct Pipe {
-  AFrag a[RING];
-  Piece<TYPE> pc[RING];
+  AFrag a[kARing<TYPE>];
+  Piece<TYPE> pc[kWRing<TYPE>];
 };
 
-// One pipelined step s (ring slot d = s % RING): request step s + RING - 1
-// (clamped to the last full step) into the slot of step s - 1, multiply
-// step s, dequantize step s + 1 into the other LDS buffer.
-template <int TYPE, int RING>
-__device__ __forceinline__ void gemm_step(f32x4_t (&acc)[2][4], Pipe<TYPE, RING>& pp, uint16_t* bs0, int d,
-                                          int64_t s, int64_t full, __amdgpu_buffer_rsrc_t X,
-                                          const uint32_t (&voff)[2], const Planes& P,
-                                          const typename Piece<TYPE>::Addr& pa, int h, int tid, int lane) {
-  const int64_t ahead = min(s + RING - 1, full - 1) * kBK;
-  load_a(pp.a[(d + RING - 1) % RING], X, voff, ahead + 64 * h);
-  pp.pc[(d + RING - 1) % RING].load(P, pa, ahead);
-  mfma_step(acc, pp.a[d], bs0 + (s & 1) * (kBN * kPitch), h, lane);
-  store_b<TYPE>(pp.pc[(d + 1) % RING], pa, bs0 + ((s + 1) & 1) * (kBN * kPitch), tid);
-  __syncthreads();
+// Step s (d = s % 4: LDS tile of step s): request X of step s + A - 1 (A =
+// kARing, slot (s - 1) % A, free since step s - 1) and weights of step
+// s + R + 1 (R = kWRing, slot (s + 1) % R, free since step s - 1), both
+// clamped to the last full step; read step s's B operands, multiply X slot
+// s % A, dequantize step s + 2 (slot (s + 2) % R) into tile (s + 2) % 4.
+// Tile (s + 2) % 4 was last read at step s - 2 and tile s % 4 was written at
+// step s - 2, so one barrier after every odd step orders both.
+template <int TYPE>
+__device__ __forceinline__ void gemm_step(f32x4_t (&acc)[4][4], Pipe<TYPE>& pp, uint16_t* bs0, int d, int64_t s,
+                                          int64_t full, __amdgpu_buffer_rsrc_t X, const uint32_t (&voff)[4],
+                                          const Planes& P, const typename Piece<TYPE>::Addr& pa, int q, int tid,
+                                          int lane) {
+  constexpr int A = kARing<TYPE>, R = kWRing<TYPE>;
+  load_a(pp.a[(d + A - 1) % A], X, voff, min(s + A - 1, full - 1) * kBK + 32 * q);
+  pp.pc[(d + 1) % R].load(P, pa, min(s + R + 1, full - 1) * kBK);
+  BFrag b;
+  read_bfrag(b, bs0 + d * kBTile, q, lane);
+  mfma_step(acc, pp.a[d % A], b);
+  store_b<TYPE>(pp.pc[(d + 2) % R], pa, bs0 + ((d + 2) % kRing) * kBTile, tid);
+  __builtin_amdgcn_sched_barrier(0);
+  if (d & 1) __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
 }
 
-// 8 waves: wave w computes rows 32 (w % 4) .. + 31 of the tile over the
-// k-half h = w / 4 of every step; the two halves are summed through LDS at
-// the end. The two waves of a SIMD (w and w + 4) share rows, so each SIMD
-// interleaves two instruction streams over the same MFMA tiles.
-template <int TYPE, int RING, bool F32_OUT>
+template <int TYPE, bool F32_OUT>
 __global__ void __launch_bounds__(kThreads) gemm_kernel(const uint8_t* __restrict__ w, int64_t n_rows, int64_t k,
-                                                        const uint16_t* __restrict__ x, int64_t ldx, int64_t m,
+                                                        const uint16_t* __restrict__ xp, int64_t m,
                                                         void* __restrict__ y, int64_t ldy, int64_t n_tiles_n) {
-  __shared__ __align__(16) uint16_t Bs[2 * kBN * kPitch];
+  // Four weight tiles during the loop; the k-quarter partial sums after it.
+  __shared__ __align__(16) float smem[kRedFloats];
+  uint16_t* Bs = reinterpret_cast<uint16_t*>(smem);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int mw = wave & 3, h = wave >> 2;
+  const int mw = wave & 1, q = wave >> 1;
   const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
   const int64_t m0 = (tile / n_tiles_n) * kBM, n0 = (tile % n_tiles_n) * kBN;
-  const int64_t row0 = m0 + 32 * mw;
+  const int64_t row0 = m0 + 64 * mw;
   const int64_t nb = k / block_elems(TYPE);
   const int64_t full = k / kBK;
   const int tail = static_cast<int>(k - full * kBK);  // 0, 32, 64 or 96
 
-  const __amdgpu_buffer_rsrc_t X = buffer_rsrc(x, static_cast<uint32_t>(m * ldx * 2));
-  uint32_t voff[2];
+  const int64_t kk_n = k >> 5, mb_n = (m + 15) >> 4;
+  const __amdgpu_buffer_rsrc_t X = buffer_rsrc(xp, static_cast<uint32_t>(mb_n * kk_n * 1024));
+  uint32_t voff[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-    voff[i] = static_cast<uint32_t>((min(row0 + 16 * i + (lane & 15), m - 1) * ldx + 8 * (lane >> 4)) * 2);
+  for (int i = 0; i < 4; ++i)
+    voff[i] = static_cast<uint32_t>(min((row0 >> 4) + i, mb_n - 1) * kk_n * 1024 + lane * 16);
   const Planes P = make_planes<TYPE>(w, n_rows, nb);
   const typename Piece<TYPE>::Addr pa = Piece<TYPE>::addr(min(n0 + (tid >> 3), n_rows - 1), nb, tid & 7);
 
-  f32x4_t acc[2][4];
+  f32x4_t acc[4][4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   if (full > 0) {
-    // Ring slot s % RING holds step s's X fragments and packed weights; step
-    // s's weights are dequantized into buffer s & 1 during step s - 1.
-    Pipe<TYPE, RING> pp;
+    constexpr int A = kARing<TYPE>, R = kWRing<TYPE>;
+    Pipe<TYPE> pp;
 #pragma unroll
-    for (int i = 0; i < RING - 1; ++i) {
-      const int64_t k0 = min<int64_t>(i, full - 1) * kBK;
-      load_a(pp.a[i], X, voff, k0 + 64 * h);
-      pp.pc[i].load(P, pa, k0);
-    }
+    for (int i = 0; i < A - 1; ++i) load_a(pp.a[i], X, voff, min<int64_t>(i, full - 1) * kBK + 32 * q);
+#pragma unroll
+    for (int i = 0; i < R; ++i) pp.pc[i].load(P, pa, min<int64_t>(i, full - 1) * kBK);
     store_b<TYPE>(pp.pc[0], pa, Bs, tid);
+    store_b<TYPE>(pp.pc[1], pa, Bs + kBTile, tid);
+    pp.pc[0].load(P, pa, min<int64_t>(R, full - 1) * kBK);
     __syncthreads();
     int64_t s0 = 0;
-    for (; s0 + RING <= full; s0 += RING) {
+    for (; s0 + kRing <= full; s0 += kRing) {
 #pragma unroll
-      for (int d = 0; d < RING; ++d)
-        gemm_step<TYPE, RING>(acc, pp, Bs, d, s0 + d, full, X, voff, P, pa, h, tid, lane);
+      for (int d = 0; d < kRing; ++d) gemm_step<TYPE>(acc, pp, Bs, d, s0 + d, full, X, voff, P, pa, q, tid, lane);
     }
 #pragma unroll
-    for (int d = 0; d < RING - 1; ++d) {
-      if (s0 + d < full) gemm_step<TYPE, RING>(acc, pp, Bs, d, s0 + d, full, X, voff, P, pa, h, tid, lane);
+    for (int d = 0; d < kRing - 1; ++d) {
+      if (s0 + d < full) gemm_step<TYPE>(acc, pp, Bs, d, s0 + d, full, X, voff, P, pa, q, tid, lane);
     }
+    __syncthreads();
   }
   if (tail > 0) {
-    // k tail of 32, 64 or 96: pieces past it and X sub-steps past it are zero.
+    // k tail of 32, 64 or 96: pieces past it and k-quarters past it are zero.
     Piece<TYPE> pt;
     AFrag at;
     if (16 * (tid & 7) < tail)
       pt.load(P, pa, full * kBK);
     else
       pt.zero();
-    load_a(at, X, voff, full * kBK + 64 * h, min(2, max(0, tail / 32 - 2 * h)));
+    load_a(at, X, voff, full * kBK + 32 * q, 32 * q < tail);
     store_b<TYPE>(pt, pa, Bs, tid);
     __syncthreads();
-    mfma_step(acc, at, Bs, h, lane);
+    BFrag bt;
+    read_bfrag(bt, Bs, q, lane);
+    mfma_step(acc, at, bt);
     __syncthreads();
   }
 
-  // Sum the two k-halves: waves 4..7 park their accumulators in LDS (the
-  // weight buffers are free after the last barrier), waves 0..3 add them.
-  float* red = reinterpret_cast<float*>(Bs) + mw * (2 * 4 * 4 * 64);
-  if (h == 1) {
+  // Sum the k-quarters: wave (mw, q) owns output m-block q of its 64 rows.
+  // It parks its other three m-blocks in LDS (slot: the writer's rank among
+  // the three non-owners), then adds the three partials of its own block.
+  float* red = smem;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[((i * 4 + j) * 4 + e) * 64 + lane] = acc[i][j][e];
-  }
-  __syncthreads();
-  if (h == 1) return;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i) {
+    if (i == q) continue;
+    float* dst = red + ((mw * 4 + i) * 3 + (q < i ? q : q - 1)) * (16 * 64);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[i][j][e] += red[((i * 4 + j) * 4 + e) * 64 + lane];
+      for (int e = 0; e < 4; ++e) dst[(j * 4 + e) * 64 + lane] = acc[i][j][e];
+  }
+  __syncthreads();
+  f32x4_t out[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i != q) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) out[j] = acc[i][j];
+  }
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const float* src = red + ((mw * 4 + q) * 3 + t) * (16 * 64);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[j][e] += src[(j * 4 + e) * 64 + lane];
+  }
 
   // Accumulator layout: lane l holds D[4 (l / 16) + e][l % 16], e < 4.
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int j = 0; j < 4; ++j) {
+    const int64_t gn = n0 + 16 * j + (lane & 15);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t gn = n0 + 16 * j + (lane & 15);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t gm = row0 + 16 * i + 4 * (lane >> 4) + e;
-        if (gm < m && gn < n_rows) {
-          if constexpr (F32_OUT)
-            static_cast<float*>(y)[gm * ldy + gn] = acc[i][j][e];
-          else
-            static_cast<__bf16*>(y)[gm * ldy + gn] = static_cast<__bf16>(acc[i][j][e]);
-        }
+    for (int e = 0; e < 4; ++e) {
+      const int64_t gm = row0 + 16 * q + 4 * (lane >> 4) + e;
+      if (gm < m && gn < n_rows) {
+        if constexpr (F32_OUT)
+          static_cast<float*>(y)[gm * ldy + gn] = out[j][e];
+        else
+          static_cast<__bf16*>(y)[gm * ldy + gn] = static_cast<__bf16>(out[j][e]);
       }
     }
   }
 }
 
+// Rows of X per launch: the packed chunk (rows rounded up to 16, times k
+// bf16) stays below 2 GiB so buffer offsets fit in 32 bits.
+int64_t chunk_rows(int64_t k) { return std::max<int64_t>(kBM, (kMaxBufferBytes / (k * 2)) / kBM * kBM); }
+
 template <int TYPE>
 int launch_gemm(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
-                int y_type, int64_t ldy, hipStream_t s) {
+                int y_type, int64_t ldy, uint16_t* xp, hipStream_t s) {
   // Weight planes are addressed with 32-bit offsets (the largest plane is at
-  // most 16/18 of the tensor); X is launched in chunks of rows that keep its
-  // offsets below 2 GiB.
+  // most 16/18 of the tensor).
   if (spiral_tensor_bytes(TYPE, n_rows, k) >= kMaxBufferBytes * 2) return SPIRAL_ERR_SHAPE;
-  const int64_t chunk = std::max<int64_t>(kBM, (kMaxBufferBytes / (ldx * 2)) / kBM * kBM);
+  const int64_t chunk = chunk_rows(k);
   const int64_t tn = ceil_div(n_rows, kBN);
   const uint8_t* W = static_cast<const uint8_t*>(w);
   const int64_t ysz = y_type == SPIRAL_TYPE_F32 ? 4 : 2;
   for (int64_t mo = 0; mo < m; mo += chunk) {
     const int64_t mc = std::min(chunk, m - mo);
     const int64_t tm = ceil_div(mc, kBM);
-    if (tn * tm > INT32_MAX) return SPIRAL_ERR_SHAPE;
+    const int64_t packs = ceil_div(mc, 16) * ceil_div(k >> 5, 16);
+    if (tn * tm > INT32_MAX || packs > INT32_MAX) return SPIRAL_ERR_SHAPE;
+    hipLaunchKernelGGL(pack_x_kernel, dim3(static_cast<unsigned>(packs)), dim3(256), 0, s, x + mo * ldx, ldx, mc, k,
+                       xp);
+    int rc = launch_status();
+    if (rc != SPIRAL_OK) return rc;
     const dim3 grid(static_cast<unsigned>(tn * tm));
-    const uint16_t* xc = x + mo * ldx;
     void* yc = static_cast<uint8_t*>(y) + mo * ldy * ysz;
     if (y_type == SPIRAL_TYPE_F32)
-      hipLaunchKernelGGL((gemm_kernel<TYPE, kRing, true>), grid, dim3(kThreads), 0, s, W, n_rows, k, xc, ldx, mc, yc, ldy, tn);
+      hipLaunchKernelGGL((gemm_kernel<TYPE, true>), grid, dim3(kThreads), 0, s, W, n_rows, k, xp, mc, yc, ldy, tn);
     else
-      hipLaunchKernelGGL((gemm_kernel<TYPE, kRing, false>), grid, dim3(kThreads), 0, s, W, n_rows, k, xc, ldx, mc, yc, ldy, tn);
-    const int rc = launch_status();
+      hipLaunchKernelGGL((gemm_kernel<TYPE, false>), grid, dim3(kThreads), 0, s, W, n_rows, k, xp, mc, yc, ldy, tn);
+    rc = launch_status();
     if (rc != SPIRAL_OK) return rc;
   }
   return SPIRAL_OK;
@@ -262,14 +322,22 @@ int launch_gemm(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int
 
 }  // namespace
 
+// Workspace for the packed X of one launch chunk.
+int64_t gemm_workspace_bytes(int64_t m, int64_t k) {
+  const int64_t rows = std::min(m, chunk_rows(k));
+  return ceil_div(rows, 16) * 16 * k * 2;
+}
+
 // Y = X W^T; arguments validated by the caller (k a multiple of the block, x
-// rows 16-byte aligned with ldx a multiple of 8).
-int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m,
-         void* y, int y_type, int64_t ldy, hipStream_t s) {
+// rows 16-byte aligned with ldx a multiple of 8, workspace of at least
+// gemm_workspace_bytes(m, k) bytes, 16-byte aligned).
+int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
+         int y_type, int64_t ldy, void* workspace, hipStream_t s) {
+  uint16_t* xp = static_cast<uint16_t*>(workspace);
   switch (type) {
-    case SPIRAL_TYPE_Q4_0: return launch_gemm<SPIRAL_TYPE_Q4_0>(w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
-    case SPIRAL_TYPE_Q8_0: return launch_gemm<SPIRAL_TYPE_Q8_0>(w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
-    case SPIRAL_TYPE_Q6_K: return launch_gemm<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
+    case SPIRAL_TYPE_Q4_0: return launch_gemm<SPIRAL_TYPE_Q4_0>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
+    case SPIRAL_TYPE_Q8_0: return launch_gemm<SPIRAL_TYPE_Q8_0>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
+    case SPIRAL_TYPE_Q6_K: return launch_gemm<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
     default: return SPIRAL_ERR_TYPE;
   }
 }

@@ -71,17 +71,27 @@ def get_rows(qtype, w, n_rows, k, ids, out_dtype=torch.float32):
     return out
 
 
-def mul_mat(qtype, w, n_rows, k, x, out_dtype=torch.bfloat16, out=None):
+def mul_mat_workspace(qtype, n_rows, k, m, device):
+    """Device workspace for mul_mat (None when the GEMV runs, which needs none)."""
+    n = lib().spiral_mul_mat_workspace_bytes(qtype, n_rows, k, m)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def mul_mat(qtype, w, n_rows, k, x, out_dtype=torch.bfloat16, out=None, workspace=None):
     """y[m, n] = sum_k x[m, k] W[n, k]; x is [m, k] bfloat16 (row stride any
-    multiple of 8)."""
+    multiple of 8). workspace: from mul_mat_workspace (allocated here when
+    omitted and needed)."""
     _require_cuda(w, x)
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("x must be a 2-D bfloat16 tensor with contiguous rows")
     m = x.shape[0]
     if out is None:
         out = torch.empty((m, n_rows), dtype=out_dtype, device=w.device)
+    if workspace is None:
+        workspace = mul_mat_workspace(qtype, n_rows, k, m, w.device)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel() * workspace.element_size())
     check(lib().spiral_mul_mat(qtype, _ptr(w), n_rows, k, _ptr(x), x.stride(0), m, _ptr(out),
-                               _out_type(out.dtype), out.stride(0), _stream()), "mul_mat")
+                               _out_type(out.dtype), out.stride(0), ws_ptr, ws_bytes, _stream()), "mul_mat")
     return out
 
 
