@@ -7,7 +7,7 @@
 Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
 x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
 workloads under "workloads": Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
-(4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096) and the Q4_0 MoE
+and Q6_K -> bf16 dequant (4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096) and the Q4_0 MoE
 grouped GEMM (128 experts, 64 tokens, top-8).
 
 Measurement
@@ -122,6 +122,7 @@ TRAFFIC_KERNELS = {
     "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
     "gemv_q4_0": (["gemv_kernel<2,"], 4096 * 4096 // 32 * 18 + 4096 * 2 + 4096 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
+    "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
     "moe_q4_0": (["moe_kernel<2,", "route_kernel"], None),
 }
@@ -290,6 +291,22 @@ def main():
                {"workload": "Q4_0 -> bf16 dequant, 4096x4096 (524,288 blocks)",
                 "bytes_per_launch": inb + outb, "packed_bytes": inb, "copies": copies})
         results["dequant_q4_0"]["packed_GBps"] = inb / (ev / steps) / 1e9
+        del ws, outs
+
+    # --- Q6_K -> bf16 dequant ---------------------------------------------------
+    if want("dequant_q6_k"):
+        n, k = 4096, 14336
+        inb = n * row_bytes(TYPE_Q6_K, k)
+        outb = n * k * 2
+        copies = copies_for(inb + outb)
+        _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies)
+        outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+        wall, ev = timer.run(lambda i: ops.dequant(TYPE_Q6_K, ws[i % copies], n, k, out=outs[i % copies]),
+                               steps, warmup)
+        record("dequant_q6_k", wall, ev, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q6_K -> bf16 dequant, 4096x14336 (229,376 super-blocks)",
+                "bytes_per_launch": inb + outb, "packed_bytes": inb, "copies": copies})
+        results["dequant_q6_k"]["packed_GBps"] = inb / (ev / steps) / 1e9
         del ws, outs
 
     # --- Q4_0 dequant-GEMM, M = 512 ---------------------------------------------

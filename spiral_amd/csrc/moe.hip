@@ -1,11 +1,15 @@
 // Grouped dequant-GEMM for mixture-of-experts (ggml MUL_MAT_ID with
 // quantized, expert-stacked weights).
 //
-// Two launches on the caller's stream:
-//  1. route_kernel (one workgroup): a counting sort of the (token, slot)
-//     pairs by expert id into per-expert lists in the caller's workspace;
-//     pairs with an out-of-range id get a zero output row.
-//  2. moe_kernel: workgroup (n-tile of 64 rows, expert) streams those weight
+// Routing: at decode sizes (at most kFusedPairs (token, slot) pairs) each
+// moe_kernel workgroup scans the ids for its own expert into LDS, and the
+// workgroups of expert 0 also write the zero rows of pairs whose id is out
+// of range: one launch. Larger batches first run route_kernel (one
+// workgroup): a counting sort of the pairs by expert id into per-expert
+// lists in the caller's workspace, pairs with an out-of-range id getting a
+// zero output row.
+//
+// moe_kernel: workgroup (n-tile of 64 rows, expert) streams those weight
 //     rows and multiplies them against the tokens routed to the expert, 16
 //     tokens (one MFMA row block) per pass. At decode batch sizes (a few
 //     tokens per expert) that is one pass, so each expert's weights are read
@@ -14,15 +18,17 @@
 // moe_kernel layout (gfx950, v_mfma_f32_16x16x32_bf16):
 //  - Wave w owns weight rows n0 + 16 w .. + 15 (the MFMA B columns). Lane l
 //    serves row l % 16 and k-group g = l / 16. For every 128-wide k step it
-//    loads one piece per lane (Q4_0 / Q8_0: block 4 kb + g; Q6_K: 32-element
-//    group g of the half super-block) straight from HBM and dequantizes it
-//    into the B operands of the step's four MFMAs, so weights never touch
-//    LDS. Pieces are requested kMoeRing - 1 steps ahead (register ring).
+//    takes one piece (Q4_0 / Q8_0: block 4 kb + g; Q6_K: 32-element group g
+//    of the half super-block) and dequantizes it into the B operands of the
+//    step's four MFMAs, so weights are never stored as bf16.
+//  - The pieces come from LDS: pairs of k steps of the workgroup's 64 rows
+//    are loaded with whole-line loads kStageAhead pairs ahead (register
+//    ring) and written to one of two LDS stages (see WStage).
 //  - An MFMA sums over its 32 k in any order as long as A and B agree; MFMA
 //    s of a step takes, from lane group g, the 8 elements of piece g that
 //    are cheapest to unpack (see MoePiece). The routed tokens' activations
-//    are staged per 1024-wide k chunk in LDS in exactly that order (only the
-//    pass's real token rows; MFMA rows past them read a copy and their
+//    are staged per kMoeKC-wide k chunk in LDS in exactly that order (only
+//    the pass's real token rows; MFMA rows past them read a copy and their
 //    outputs are dropped).
 // Products use exactly dequantized bf16 weights and fp32 accumulation, as in
 // the dense GEMM.
@@ -142,7 +148,12 @@ template <>
 struct MoePiece<SPIRAL_TYPE_Q4_0> {
   uint4 q;
   uint32_t d;
+  float m, off;  // decoded scale and offset (prep)
   static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
+  __device__ __forceinline__ void prep() {
+    m = fp16_scale(d);
+    off = -1032.0f * m;
+  }
   // blk = block index of the lane's piece within the row's planar planes
   __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t blk) {
     q = *reinterpret_cast<const uint4*>(we + blk * 16);
@@ -151,7 +162,7 @@ struct MoePiece<SPIRAL_TYPE_Q4_0> {
   __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
   __device__ __forceinline__ uint4 dequant(int s) const {
     const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
-    const float df = fp16_scale(d), off = -1032.0f * df;
+    const float df = m;
     const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
     uint32_t o[4];
 #pragma unroll
@@ -171,7 +182,12 @@ template <>
 struct MoePiece<SPIRAL_TYPE_Q8_0> {
   uint4 q0, q1;
   uint32_t d;
+  float m, off;  // decoded scale and offset (prep)
   static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + 8 * s + e; }
+  __device__ __forceinline__ void prep() {
+    m = fp16_scale(d);
+    off = -1152.0f * m;
+  }
   __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t blk) {
     q0 = *reinterpret_cast<const uint4*>(we + blk * 32);
     q1 = *reinterpret_cast<const uint4*>(we + blk * 32 + 16);
@@ -181,7 +197,7 @@ struct MoePiece<SPIRAL_TYPE_Q8_0> {
   __device__ __forceinline__ uint4 dequant(int s) const {
     const uint32_t w0 = (s == 0 ? q0.x : s == 1 ? q0.z : s == 2 ? q1.x : q1.z) ^ 0x80808080u;
     const uint32_t w1 = (s == 0 ? q0.y : s == 1 ? q0.w : s == 2 ? q1.y : q1.w) ^ 0x80808080u;
-    const float df = fp16_scale(d), off = -1152.0f * df;
+    const float df = m;
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -203,6 +219,14 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
   uint4 l0, l1, h0, h1;
   uint32_t ds2;  // fp16 d (bits 0..15), sc for l < 16 (16..23), sc for l >= 16 (24..31)
   int ls, hs;
+  float m0, off0, m1, off1;  // d * sc and offsets for l < 16 and l >= 16 (prep)
+  __device__ __forceinline__ void prep() {
+    const float d = fp16_scale(ds2 & 0xffffu);
+    m0 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 16));
+    m1 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 24));
+    off0 = -32.0f * m0;
+    off1 = -32.0f * m1;
+  }
   static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + 8 * s + e; }
   // sb_row = super-block index (row * nb + sb), h = half, g = group
   __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t sbi, int h, int g) {
@@ -222,8 +246,8 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
     const uint4 L = s < 2 ? l0 : l1, H = s < 2 ? h0 : h1;
     const uint32_t wl0 = (s & 1) ? L.z : L.x, wl1 = (s & 1) ? L.w : L.y;
     const uint32_t wh0 = (s & 1) ? H.z : H.x, wh1 = (s & 1) ? H.w : H.y;
-    const float ds = fp16_scale(ds2 & 0xffffu) * static_cast<float>(static_cast<int8_t>(ds2 >> (s < 2 ? 16 : 24)));
-    const float off = -32.0f * ds;
+    const float ds = s < 2 ? m0 : m1;
+    const float off = s < 2 ? off0 : off1;
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -237,23 +261,154 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
   }
 };
 
-constexpr int kMoeKC = 1024;                  // k chunk of activations staged in LDS
+constexpr int kMoeKC = 768;                   // k chunk of activations staged in LDS (3 pairs)
 constexpr int kMoeTok = 16;                   // tokens per pass (one MFMA row block)
 constexpr int kMoeAPitch = kMoeKC + 8;        // bf16 per staged row
-constexpr int kMoeRing = 4;                   // 128-wide k steps of weights in flight
+constexpr int kFusedPairs = 1024;             // largest batch routed inside moe_kernel
+constexpr int kStageAhead = 3;                // weight pairs in flight in registers
+static_assert(kMoeKC % 256 == 0, "activation chunks hold whole weight pairs");
 
-// Pieces of k step `st` (128 wide) for this lane's row n and group g.
+// ---- weights staged through LDS -------------------------------------------
+//
+// A stage is one pair of 128-wide k steps (256 k) of the workgroup's 64
+// weight rows. Each thread loads its share with whole-line loads (8 or 16
+// lanes per 128-byte line of a row) into registers kStageAhead pairs ahead,
+// writes it to an LDS stage, and each wave then reads its MFMA pieces (16
+// rows x 4 lane groups) from LDS. Loading the pieces directly would touch
+// 16 rows per instruction, 16 or 2 bytes of each. Offsets are 32-bit (the
+// launcher keeps each expert matrix below 2 GiB); rows past n_rows are
+// clamped (their outputs are never stored) and blocks past k read as zero.
 template <int TYPE>
-__device__ __forceinline__ void moe_load(MoePiece<TYPE>& pc, const uint8_t* we, int64_t n_rows, int64_t nb,
-                                         int64_t n, int64_t k, int64_t st, int g) {
-  if constexpr (TYPE == SPIRAL_TYPE_Q6_K) {
-    pc.load(we, n_rows * nb, n * nb + (st >> 1), static_cast<int>(st & 1), g);
-  } else {
-    const int64_t b = 4 * st + g;
-    if (32 * b >= k) { pc.zero(); return; }
-    pc.load(we, n_rows * nb, n * nb + b);
+struct WStage;
+
+// Q4_0 pair: per row 8 blocks, qs 128 bytes (LDS pitch 144) and d 16 bytes.
+template <>
+struct WStage<SPIRAL_TYPE_Q4_0> {
+  static constexpr int kQsPitch = 144, kDOff = 64 * kQsPitch, kBytes = kDOff + 64 * 16;
+  struct Addr {
+    uint32_t q[2], d;
+    int qc, dc;
+  };
+  uint4 q[2];
+  uint32_t d0, d1;
+  // thread t: qs of rows 32 i + t / 8 (i < 2), block t % 8; d of row t / 4,
+  // blocks 2 (t % 4) and 2 (t % 4) + 1.
+  static __device__ __forceinline__ Addr addr(int64_t n0, int64_t n_rows, int64_t nb, int t) {
+    Addr a;
+    for (int i = 0; i < 2; ++i)
+      a.q[i] = static_cast<uint32_t>((min(n0 + 32 * i + t / 8, n_rows - 1) * nb + t % 8) * 16);
+    a.qc = t % 8;
+    a.dc = 2 * (t % 4);
+    a.d = static_cast<uint32_t>((min(n0 + t / 4, n_rows - 1) * nb + a.dc) * 2);
+    return a;
   }
-}
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t p, int64_t nb) {
+    const int64_t b = 8 * p;
+    const uint32_t sq = static_cast<uint32_t>(b * 16), sd = static_cast<uint32_t>(b * 2);
+    const bool qv = b + a.qc < nb;
+    for (int i = 0; i < 2; ++i) q[i] = qv ? bload16(P.a, a.q[i], sq) : make_uint4(0u, 0u, 0u, 0u);
+    d0 = b + a.dc < nb ? bload2(P.d, a.d, sd) : 0u;
+    d1 = b + a.dc + 1 < nb ? bload2(P.d, a.d + 2, sd) : 0u;
+  }
+  __device__ __forceinline__ void store(uint8_t* st, int t) const {
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(st + (32 * i + t / 8) * kQsPitch + (t % 8) * 16) = q[i];
+    *reinterpret_cast<uint32_t*>(st + kDOff + (t / 4) * 16 + (t % 4) * 4) = d0 | (d1 << 16);
+  }
+  // Piece of row r (0..63) for step h (0, 1) of the pair and lane group g.
+  static __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& pc, const uint8_t* st, int r, int h, int g) {
+    pc.q = *reinterpret_cast<const uint4*>(st + r * kQsPitch + (4 * h + g) * 16);
+    pc.d = *reinterpret_cast<const uint16_t*>(st + kDOff + r * 16 + (4 * h + g) * 2);
+  }
+};
+
+// Q8_0 pair: per row 8 blocks, qs 256 bytes (LDS pitch 272) and d 16 bytes.
+template <>
+struct WStage<SPIRAL_TYPE_Q8_0> {
+  static constexpr int kQsPitch = 272, kDOff = 64 * kQsPitch, kBytes = kDOff + 64 * 16;
+  struct Addr {
+    uint32_t q[4], d;
+    int qc, dc;
+  };
+  uint4 q[4];
+  uint32_t d0, d1;
+  // thread t: qs bytes 16 (t % 16) .. + 15 of rows 16 i + t / 16 (i < 4).
+  static __device__ __forceinline__ Addr addr(int64_t n0, int64_t n_rows, int64_t nb, int t) {
+    Addr a;
+    for (int i = 0; i < 4; ++i)
+      a.q[i] = static_cast<uint32_t>(min(n0 + 16 * i + t / 16, n_rows - 1) * nb * 32 + (t % 16) * 16);
+    a.qc = (t % 16) / 2;
+    a.dc = 2 * (t % 4);
+    a.d = static_cast<uint32_t>((min(n0 + t / 4, n_rows - 1) * nb + a.dc) * 2);
+    return a;
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t p, int64_t nb) {
+    const int64_t b = 8 * p;
+    const uint32_t sq = static_cast<uint32_t>(b * 32), sd = static_cast<uint32_t>(b * 2);
+    const bool qv = b + a.qc < nb;
+    for (int i = 0; i < 4; ++i) q[i] = qv ? bload16(P.a, a.q[i], sq) : make_uint4(0u, 0u, 0u, 0u);
+    d0 = b + a.dc < nb ? bload2(P.d, a.d, sd) : 0u;
+    d1 = b + a.dc + 1 < nb ? bload2(P.d, a.d + 2, sd) : 0u;
+  }
+  __device__ __forceinline__ void store(uint8_t* st, int t) const {
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(st + (16 * i + t / 16) * kQsPitch + (t % 16) * 16) = q[i];
+    *reinterpret_cast<uint32_t*>(st + kDOff + (t / 4) * 16 + (t % 4) * 4) = d0 | (d1 << 16);
+  }
+  static __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q8_0>& pc, const uint8_t* st, int r, int h, int g) {
+    pc.q0 = *reinterpret_cast<const uint4*>(st + r * kQsPitch + (4 * h + g) * 32);
+    pc.q1 = *reinterpret_cast<const uint4*>(st + r * kQsPitch + (4 * h + g) * 32 + 16);
+    pc.d = *reinterpret_cast<const uint16_t*>(st + kDOff + r * 16 + (4 * h + g) * 2);
+  }
+};
+
+// Q6_K pair: one super-block per row: ql 128 bytes (pitch 144), qh 64 (pitch
+// 80), sc 16, d 2.
+template <>
+struct WStage<SPIRAL_TYPE_Q6_K> {
+  static constexpr int kQhOff = 64 * 144, kScOff = kQhOff + 64 * 80, kDOff = kScOff + 64 * 16, kBytes = kDOff + 64 * 2;
+  struct Addr {
+    uint32_t l[2], h, sc, d;
+  };
+  uint4 l[2], h;
+  uint32_t sc, d;
+  // thread t: ql bytes 16 (t % 8) of rows 32 i + t / 8; qh bytes 16 (t % 4)
+  // and sc bytes 4 (t % 4) of row t / 4; d of row t (t < 64).
+  static __device__ __forceinline__ Addr addr(int64_t n0, int64_t n_rows, int64_t nb, int t) {
+    Addr a;
+    for (int i = 0; i < 2; ++i)
+      a.l[i] = static_cast<uint32_t>(min(n0 + 32 * i + t / 8, n_rows - 1) * nb * 128 + (t % 8) * 16);
+    const int64_t r4 = min(n0 + t / 4, n_rows - 1) * nb;
+    a.h = static_cast<uint32_t>(r4 * 64 + (t % 4) * 16);
+    a.sc = static_cast<uint32_t>(r4 * 16 + (t % 4) * 4);
+    a.d = static_cast<uint32_t>(min(n0 + (t & 63), n_rows - 1) * nb * 2);
+    return a;
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t p, int64_t) {
+    const uint32_t sb = static_cast<uint32_t>(p);
+    for (int i = 0; i < 2; ++i) l[i] = bload16(P.a, a.l[i], sb * 128u);
+    h = bload16(P.b, a.h, sb * 64u);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b32(P.c, a.sc, sb * 16u, 0);
+    sc = static_cast<uint32_t>(v);
+    d = bload2(P.d, a.d, sb * 2u);
+  }
+  __device__ __forceinline__ void store(uint8_t* st, int t) const {
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(st + (32 * i + t / 8) * 144 + (t % 8) * 16) = l[i];
+    *reinterpret_cast<uint4*>(st + kQhOff + (t / 4) * 80 + (t % 4) * 16) = h;
+    *reinterpret_cast<uint32_t*>(st + kScOff + (t / 4) * 16 + (t % 4) * 4) = sc;
+    if (t < 64) *reinterpret_cast<uint16_t*>(st + kDOff + t * 2) = static_cast<uint16_t>(d);
+  }
+  static __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q6_K>& pc, const uint8_t* st, int r, int h, int g) {
+    const uint8_t* ql = st + r * 144 + 64 * h + 32 * (g & 1);
+    const uint8_t* qh = st + kQhOff + r * 80 + 32 * h;
+    pc.l0 = *reinterpret_cast<const uint4*>(ql);
+    pc.l1 = *reinterpret_cast<const uint4*>(ql + 16);
+    pc.h0 = *reinterpret_cast<const uint4*>(qh);
+    pc.h1 = *reinterpret_cast<const uint4*>(qh + 16);
+    const uint32_t sc = *reinterpret_cast<const uint16_t*>(st + kScOff + r * 16 + 8 * h + 2 * g);
+    pc.ds2 = *reinterpret_cast<const uint16_t*>(st + kDOff + r * 2) | (sc << 16);
+    pc.ls = (g >> 1) * 4;
+    pc.hs = 2 * g;
+  }
+};
 
 // Stage activations k in [c0, c0 + kMoeKC) of the pass's nt token rows in
 // MFMA order: item = 8 consecutive LDS positions (one lane group of one MFMA)
@@ -275,82 +430,142 @@ __device__ __forceinline__ void moe_stage(uint16_t* As, const uint16_t* __restri
   }
 }
 
+// offsets == nullptr: fused routing (n_pairs <= kFusedPairs) from ids;
+// otherwise the expert's pairs are list[offsets[e] .. offsets[e + 1]).
 template <int TYPE, bool F32_OUT>
 __global__ void __launch_bounds__(256) moe_kernel(const uint8_t* __restrict__ w, int64_t expert_stride,
                                                   int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
-                                                  int64_t x_slots, int64_t top_k,
+                                                  int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids,
+                                                  int32_t n_pairs, int32_t n_expert,
                                                   const int32_t* __restrict__ offsets,
                                                   const int32_t* __restrict__ list, void* __restrict__ y) {
   __shared__ __align__(16) uint16_t As[kMoeTok * kMoeAPitch];
+  __shared__ __align__(16) uint8_t Ws[2 * WStage<TYPE>::kBytes];
   __shared__ int32_t s_pair[kMoeTok];
   __shared__ int64_t s_xrow[kMoeTok];
+  __shared__ int32_t s_list[kFusedPairs];
+  __shared__ int32_t s_n;
   const int64_t e = blockIdx.y;
-  const int32_t begin = offsets[e], end = offsets[e + 1];
-  if (begin >= end) return;
   const int tid = threadIdx.x, lane = tid & 63;
+  int32_t begin, end;
+  const int32_t* lst;
+  if (offsets == nullptr) {
+    // Fused routing: the pairs routed to e, in any order (each output row is
+    // computed on its own). Expert 0's workgroups also clear the rows of
+    // pairs routed nowhere, each over its own 64 columns.
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    for (int32_t p = tid; p < n_pairs; p += 256) {
+      const int32_t id = ids[p];
+      if (id == e) s_list[atomicAdd(&s_n, 1)] = p;
+      if (e == 0 && (id < 0 || id >= n_expert)) {
+        const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kMoeBN;
+        for (int64_t c = c0; c < min(c0 + kMoeBN, n_rows); ++c) {
+          if constexpr (F32_OUT)
+            static_cast<float*>(y)[p * n_rows + c] = 0.0f;
+          else
+            static_cast<uint16_t*>(y)[p * n_rows + c] = 0;
+        }
+      }
+    }
+    __syncthreads();
+    begin = 0;
+    end = s_n;
+    lst = s_list;
+  } else {
+    begin = offsets[e];
+    end = offsets[e + 1];
+    lst = list;
+  }
+  if (begin >= end) return;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;
-  // Rows past n_rows are clamped (their outputs are not stored).
-  const int64_t n = static_cast<int64_t>(blockIdx.x) * kMoeBN + 16 * wave + (lane & 15);
-  const int64_t nc = min(n, n_rows - 1);
-  const uint8_t* we = w + e * expert_stride;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kMoeBN;
+  const int64_t n = n0 + 16 * wave + (lane & 15);  // this lane's weight row (MFMA column)
+  const int r = 16 * wave + (lane & 15);            // its row within the stage
   const int64_t nb = k / block_elems(TYPE);
-  const int64_t steps = (k + 127) / 128;
-  constexpr int kStepsPerChunk = kMoeKC / 128;
+  const int64_t steps = (k + 127) / 128, pairs = (steps + 1) / 2;
+  constexpr int kStepsPerChunk = kMoeKC / 128, kPairsPerChunk = kMoeKC / 256;
+  const Planes P = make_planes<TYPE>(w + e * expert_stride, n_rows, nb);
+  const typename WStage<TYPE>::Addr wa = WStage<TYPE>::addr(n0, n_rows, nb, tid);
 
   for (int32_t t0 = begin; t0 < end; t0 += kMoeTok) {
     const int nt = min(kMoeTok, end - t0);
     __syncthreads();
     if (tid < kMoeTok) {
-      const int32_t pr = tid < nt ? list[t0 + tid] : -1;
+      const int32_t pr = tid < nt ? lst[t0 + tid] : -1;
       s_pair[tid] = pr;
       if (pr >= 0) {
         const int64_t t = pr / top_k, slot = pr % top_k;
         s_xrow[tid] = (t * x_slots + slot % x_slots) * k;
       }
     }
+    // Weights do not depend on the tokens: start the ring first.
+    WStage<TYPE> ring[kStageAhead];
+#pragma unroll
+    for (int i = 0; i < kStageAhead; ++i) ring[i].load(P, wa, min<int64_t>(i, pairs - 1), nb);
     __syncthreads();
     // MFMA rows past nt read row nt - 1; their outputs are dropped.
     const uint16_t* arow = As + min(lane & 15, nt - 1) * kMoeAPitch + 8 * g;
-    f32x4_t acc = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // One accumulator per MFMA of a step, so consecutive MFMAs do not wait
+    // for each other's results; summed at the end.
+    f32x4_t acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    moe_stage<TYPE>(As, x, s_xrow, nt, k, 0, tid);
+    ring[0].store(Ws, tid);
+    ring[0].load(P, wa, min<int64_t>(kStageAhead, pairs - 1), nb);
+    __syncthreads();
 
-    // Weight ring: slot st % kMoeRing holds step st's pieces.
-    MoePiece<TYPE> ring[kMoeRing];
+    // Pair p sits in LDS stage p % 2 and, before that, in ring slot
+    // p % kStageAhead. One barrier per pair orders both LDS buffers. A chunk
+    // of activations holds kStageAhead pairs, so inside it the ring slot and
+    // the activation offsets are compile-time constants.
+    static_assert(kStageAhead == kPairsPerChunk, "ring slots follow the pair index inside a chunk");
+    const int64_t chunks = (pairs + kPairsPerChunk - 1) / kPairsPerChunk;
+    for (int64_t c = 0; c < chunks; ++c) {
+      if (c > 0) {
+        moe_stage<TYPE>(As, x, s_xrow, nt, k, c * kMoeKC, tid);
+        __syncthreads();
+      }
 #pragma unroll
-    for (int i = 0; i < kMoeRing - 1; ++i) moe_load<TYPE>(ring[i], we, n_rows, nb, nc, k, min<int64_t>(i, steps - 1), g);
-
-    for (int64_t s0 = 0; s0 < steps; s0 += kMoeRing) {
+      for (int d = 0; d < kPairsPerChunk; ++d) {
+        const int64_t p = c * kPairsPerChunk + d;
+        if (p >= pairs) break;
+        const uint8_t* st = Ws + (p & 1) * WStage<TYPE>::kBytes;
 #pragma unroll
-      for (int d = 0; d < kMoeRing; ++d) {
-        const int64_t st = s0 + d;
-        if (st >= steps) break;
-        if (st % kStepsPerChunk == 0) {
-          __syncthreads();
-          moe_stage<TYPE>(As, x, s_xrow, nt, k, st * 128, tid);
-          __syncthreads();
+        for (int h = 0; h < 2; ++h) {
+          if (h == 0 || 2 * p + 1 < steps) {
+            MoePiece<TYPE> pc;
+            WStage<TYPE>::piece(pc, st, r, h, g);
+            pc.prep();
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const bf16x8_t b = __builtin_bit_cast(bf16x8_t, pc.dequant(s));
+              const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(arow + 8 * (16 * (2 * d + h) + 4 * s));
+              acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[s], 0, 0, 0);
+            }
+          }
         }
-        moe_load<TYPE>(ring[(d + kMoeRing - 1) % kMoeRing], we, n_rows, nb, nc, k,
-                       min<int64_t>(st + kMoeRing - 1, steps - 1), g);
-        const int j = static_cast<int>(st % kStepsPerChunk);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const bf16x8_t b = __builtin_bit_cast(bf16x8_t, ring[d].dequant(s));
-          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(arow + 8 * (16 * j + 4 * s));
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+        if (p + 1 < pairs) {
+          ring[(d + 1) % kStageAhead].store(Ws + ((p + 1) & 1) * WStage<TYPE>::kBytes, tid);
+          ring[(d + 1) % kStageAhead].load(P, wa, min<int64_t>(p + 1 + kStageAhead, pairs - 1), nb);
         }
+        __syncthreads();
       }
     }
 
     // acc: lane l holds rows 4 (l / 16) + i (routed pairs) of column l % 16
     // (weight row n).
+    const f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int32_t pr = s_pair[4 * g + i];
       if (pr >= 0 && n < n_rows) {
         if constexpr (F32_OUT)
-          static_cast<float*>(y)[pr * n_rows + n] = acc[i];
+          static_cast<float*>(y)[pr * n_rows + n] = sum[i];
         else
-          static_cast<__bf16*>(y)[pr * n_rows + n] = static_cast<__bf16>(acc[i]);
+          static_cast<__bf16*>(y)[pr * n_rows + n] = static_cast<__bf16>(sum[i]);
       }
     }
   }
@@ -365,22 +580,30 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
         int y_type, void* workspace, hipStream_t s) {
   const int64_t n_pairs = n_tokens * top_k;
-  int32_t* offsets = static_cast<int32_t*>(workspace);
-  int32_t* list = offsets + n_expert + 1;
   const int f32 = y_type == SPIRAL_TYPE_F32;
-  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
-                     static_cast<int32_t>(n_expert), offsets, list, y, n_rows, f32);
-  if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
+  // Weight planes of one expert are addressed with 32-bit offsets.
+  if (spiral_tensor_bytes(type, n_rows, k) >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
+  int32_t* offsets = nullptr;
+  int32_t* list = nullptr;
+  if (n_pairs > kFusedPairs) {
+    offsets = static_cast<int32_t*>(workspace);
+    list = offsets + n_expert + 1;
+    hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
+                       static_cast<int32_t>(n_expert), offsets, list, y, n_rows, f32);
+    if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
+  }
   const dim3 grid(static_cast<unsigned>(ceil_div(n_rows, kMoeBN)), static_cast<unsigned>(n_expert));
   const uint8_t* W = static_cast<const uint8_t*>(w);
 #define SPIRAL_MOE(T)                                                                                    \
   do {                                                                                                   \
     if (f32)                                                                                             \
       hipLaunchKernelGGL((moe_kernel<T, true>), grid, dim3(256), 0, s, W, expert_stride, n_rows, k, x,   \
-                         x_slots, top_k, offsets, list, y);                                              \
+                         x_slots, top_k, ids, static_cast<int32_t>(n_pairs), static_cast<int32_t>(n_expert), \
+                         offsets, list, y);                                                              \
     else                                                                                                 \
       hipLaunchKernelGGL((moe_kernel<T, false>), grid, dim3(256), 0, s, W, expert_stride, n_rows, k, x,  \
-                         x_slots, top_k, offsets, list, y);                                              \
+                         x_slots, top_k, ids, static_cast<int32_t>(n_pairs), static_cast<int32_t>(n_expert), \
+                         offsets, list, y);                                                              \
   } while (0)
   if (type == SPIRAL_TYPE_Q4_0) SPIRAL_MOE(SPIRAL_TYPE_Q4_0);
   else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE(SPIRAL_TYPE_Q8_0);

@@ -240,6 +240,24 @@ def test_moe_per_slot_inputs_and_bad_ids(cuda):
     assert not out.cpu().numpy().any()
 
 
+def test_moe_large_batch_routing_and_bad_ids(cuda):
+    """More (token, slot) pairs than the kernel routes by itself (1024): the
+    counting-sort route kernel runs first. Out-of-range ids give zero rows
+    on this path as on the fused one."""
+    y, ref, _ = _moe_case(cuda, O.Q4_0, 16, 64, 256, 160, 8, 1, 14, torch.float32)  # 1280 pairs
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W
+    qtype, n_expert, n, k = O.Q4_0, 4, 32, 64
+    per = O.row_bytes(qtype, k) * n
+    w = torch.zeros(n_expert * per, dtype=torch.uint8, device=cuda)
+    ids = torch.randint(0, n_expert, (1100, 1), dtype=torch.int32)
+    ids[::7] = -1
+    ids[3::11] = 99
+    x = torch.zeros((1100, 1, k), dtype=torch.bfloat16, device=cuda)
+    out = torch.full((1100, 1, n), 7.0, device=cuda)
+    ops.mul_mat_id(qtype, w, per, n_expert, n, k, x, ids.to(cuda), out=out)
+    assert not out.cpu().numpy().any()
+
+
 def test_moe_128_experts_gate_up(cuda):
     """The MoE workload's gate_up stage: 128 experts of 1536 x 2048 Q4_0,
     64 tokens, top-8 distinct experts per token."""
