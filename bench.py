@@ -124,7 +124,7 @@ TRAFFIC_KERNELS = {
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
-    "moe_q4_0": (["moe_kernel<2,", "route_kernel"], None),
+    "moe_q4_0": (["moe_stream_kernel<2,"], None),
 }
 
 
@@ -155,7 +155,7 @@ def write_traffic(d):
     fs, ws = kib / pick(cf, "copyBuffer"), kib / pick(cw, "copyBuffer")
     out = {"note": "HBM bytes per step: rocprofv3 FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled "
                    "so that a 256 MiB device-to-device copy reads as 262144 KiB; MoE steps are two "
-                   "MUL_MAT_ID launches (route + grouped GEMM each)",
+                   "MUL_MAT_ID launches (one grouped-GEMM kernel each at decode sizes)",
            "copy_calibration": {"bytes": 256 << 20, "fetch_kb_raw": round(kib / fs, 1),
                                 "write_kb_raw": round(kib / ws, 1), "fetch_scale": round(fs, 4),
                                 "write_scale": round(ws, 4)},

@@ -9,7 +9,13 @@
 // lists in the caller's workspace, pairs with an out-of-range id getting a
 // zero output row.
 //
-// moe_kernel: workgroup (n-tile of 64 rows, expert) streams those weight
+// moe_stream_kernel (k <= kStreamMaxK, every shape the decode path meets):
+//     a few workgroups per expert, each over a contiguous range of 16-row
+//     groups; the routed tokens' activations are staged in LDS once and the
+//     waves stream their weight rows with no barriers (see the streaming
+//     section below).
+//
+// moe_kernel (larger k): workgroup (n-tile of 64 rows, expert) streams those weight
 //     rows and multiplies them against the tokens routed to the expert, 16
 //     tokens (one MFMA row block) per pass. At decode batch sizes (a few
 //     tokens per expert) that is one pass, so each expert's weights are read
@@ -32,6 +38,8 @@
 //    outputs are dropped).
 // Products use exactly dequantized bf16 weights and fp32 accumulation, as in
 // the dense GEMM.
+#include <algorithm>
+
 #include "common.h"
 #include "dequant_impl.h"
 
@@ -415,9 +423,10 @@ struct WStage<SPIRAL_TYPE_Q6_K> {
 // of one row. Positions past k are zero.
 template <int TYPE>
 __device__ __forceinline__ void moe_stage(uint16_t* As, const uint16_t* __restrict__ x, const int64_t* xrow, int nt,
-                                          int64_t k, int64_t c0, int tid) {
-  constexpr int kItems = kMoeKC / 8;
-  for (int it = tid; it < nt * kItems; it += 256) {
+                                          int64_t k, int64_t c0, int tid, int width = kMoeKC, int pitch = kMoeAPitch,
+                                          int nthreads = 256) {
+  const int kItems = width / 8;
+  for (int it = tid; it < nt * kItems; it += nthreads) {
     const int r = it / kItems, q = it % kItems;
     const int j = q >> 4, s = (q >> 2) & 3, gg = q & 3;
     const int64_t kb = c0 + 128 * j;
@@ -426,7 +435,7 @@ __device__ __forceinline__ void moe_stage(uint16_t* As, const uint16_t* __restri
     uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
     if (kb + k0 < k) lo = *reinterpret_cast<const uint2*>(src + k0);
     if (kb + k4 < k) hi = *reinterpret_cast<const uint2*>(src + k4);
-    *reinterpret_cast<uint4*>(&As[r * kMoeAPitch + 8 * q]) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    *reinterpret_cast<uint4*>(&As[r * pitch + 8 * q]) = make_uint4(lo.x, lo.y, hi.x, hi.y);
   }
 }
 
@@ -571,6 +580,344 @@ __global__ void __launch_bounds__(256) moe_kernel(const uint8_t* __restrict__ w,
   }
 }
 
+
+// ---- streaming form (the decode path) ------------------------------------
+//
+// When the activations of 16 tokens over the whole k fit in LDS (k <= 4096)
+// the workgroup stages them once per pass of 16 tokens and its waves then run
+// without barriers: wave w takes the 16-row groups w, w + 8, ... of the
+// workgroup's row range and streams (group, k step) items end to end through
+// its own register ring of pieces, loaded straight from memory with buffer
+// loads. A few workgroups per expert (about two per CU in total) each cover a
+// contiguous range of rows, so the routing scan and the activation staging
+// are paid a few hundred times per call instead of once per 64 rows.
+constexpr int kStreamThreads = 512;  // 8 waves
+constexpr int64_t kStreamMaxK = 4096;
+
+// Ring slots (units) in flight per wave.
+template <int TYPE>
+constexpr int kStreamRing = TYPE == SPIRAL_TYPE_Q4_0 ? 4 : TYPE == SPIRAL_TYPE_Q8_0 ? 6 : 4;
+
+// A lane's piece offsets for one weight row (lane group g), and the loads
+// of k step st: the same pieces as WStage::piece reads from LDS.
+template <int TYPE>
+struct PieceAddr;
+
+template <>
+struct PieceAddr<SPIRAL_TYPE_Q4_0> {
+  uint32_t q, d;
+  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g) {
+    q = static_cast<uint32_t>((row * nb + g) * 16);
+    d = static_cast<uint32_t>((row * nb + g) * 2);
+  }
+  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_Q4_0>& pc, const Planes& P, int64_t st) const {
+    pc.q = bload16(P.a, q, static_cast<uint32_t>(st) * 64u);
+    pc.d = bload2(P.d, d, static_cast<uint32_t>(st) * 8u);
+  }
+};
+
+template <>
+struct PieceAddr<SPIRAL_TYPE_Q8_0> {
+  uint32_t q, d;
+  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g) {
+    q = static_cast<uint32_t>((row * nb + g) * 32);
+    d = static_cast<uint32_t>((row * nb + g) * 2);
+  }
+  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_Q8_0>& pc, const Planes& P, int64_t st) const {
+    pc.q0 = bload16(P.a, q, static_cast<uint32_t>(st) * 128u);
+    pc.q1 = bload16(P.a, q + 16u, static_cast<uint32_t>(st) * 128u);
+    pc.d = bload2(P.d, d, static_cast<uint32_t>(st) * 8u);
+  }
+};
+
+template <>
+struct PieceAddr<SPIRAL_TYPE_Q6_K> {
+  uint32_t l, h, sc, d;
+  int g;
+  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g_) {
+    g = g_;
+    l = static_cast<uint32_t>(row * nb * 128 + 32 * (g & 1));
+    h = static_cast<uint32_t>(row * nb * 64);
+    sc = static_cast<uint32_t>(row * nb * 16 + 2 * g);
+    d = static_cast<uint32_t>(row * nb * 2);
+  }
+  // Step st is half st % 2 of super-block st / 2.
+  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_Q6_K>& pc, const Planes& P, int64_t st) const {
+    const uint32_t sb = static_cast<uint32_t>(st >> 1), hh = static_cast<uint32_t>(st & 1);
+    pc.l0 = bload16(P.a, l, sb * 128u + 64u * hh);
+    pc.l1 = bload16(P.a, l + 16u, sb * 128u + 64u * hh);
+    pc.h0 = bload16(P.b, h, sb * 64u + 32u * hh);
+    pc.h1 = bload16(P.b, h + 16u, sb * 64u + 32u * hh);
+    const uint32_t scv = bload2(P.c, sc, sb * 16u + 8u * hh);
+    pc.ds2 = bload2(P.d, d, sb * 2u) | (scv << 16);
+    pc.ls = (g >> 1) * 4;
+    pc.hs = 2 * g;
+  }
+};
+
+// What one ring slot of the streaming form holds (a "unit"), loaded for one
+// 16-row group of the wave. Q4_0: a pair of k steps of all 16 rows, loaded
+// as whole 128-byte lines (lanes 8 r' + c: row r', block c of the pair, in
+// two instructions for rows 0..7 and 8..15) and moved into MFMA position
+// with ds_bpermute; loading the pieces directly would fetch every line as
+// two 64-byte halves, which the L1's miss capacity turns into the limit.
+// Other types: one k step's pieces, loaded directly.
+template <int TYPE>
+struct Unit {
+  static constexpr int kSteps = 1;
+  MoePiece<TYPE> pc;
+  struct Addr {
+    PieceAddr<TYPE> pa;
+  };
+  static __device__ __forceinline__ Addr addr(int64_t row0, int64_t n_rows, int64_t nb, int lane) {
+    Addr a;
+    a.pa.set(min(row0 + (lane & 15), n_rows - 1), nb, lane >> 4);
+    return a;
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t) { a.pa.load(pc, P, u); }
+  __device__ __forceinline__ void piece(MoePiece<TYPE>& out, int, int) const { out = pc; }
+};
+
+template <>
+struct Unit<SPIRAL_TYPE_Q4_0> {
+  static constexpr int kSteps = 2;
+  uint4 qa, qb;  // rows lane / 8 and 8 + lane / 8 of the group, block 8 u + lane % 8
+  uint32_t dd;   // row lane / 4: d of blocks 8 u + 2 (lane % 4) (low half) and + 1
+  struct Addr {
+    uint32_t qa, qb, d;
+    int c, dc;
+  };
+  static __device__ __forceinline__ Addr addr(int64_t row0, int64_t n_rows, int64_t nb, int lane) {
+    Addr a;
+    a.c = lane & 7;
+    a.dc = 2 * (lane & 3);
+    a.qa = static_cast<uint32_t>((min(row0 + (lane >> 3), n_rows - 1) * nb + a.c) * 16);
+    a.qb = static_cast<uint32_t>((min(row0 + 8 + (lane >> 3), n_rows - 1) * nb + a.c) * 16);
+    a.d = static_cast<uint32_t>((min(row0 + (lane >> 2), n_rows - 1) * nb + a.dc) * 2);
+    return a;
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t nb) {
+    const int64_t b = 8 * u;
+    const uint32_t sq = static_cast<uint32_t>(b * 16), sd = static_cast<uint32_t>(b * 2);
+    const bool qv = b + a.c < nb;
+    qa = qv ? bload16(P.a, a.qa, sq) : make_uint4(0u, 0u, 0u, 0u);
+    qb = qv ? bload16(P.a, a.qb, sq) : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t d0 = b + a.dc < nb ? bload2(P.d, a.d, sd) : 0u;
+    const uint32_t d1 = b + a.dc + 1 < nb ? bload2(P.d, a.d + 2, sd) : 0u;
+    dd = d0 | (d1 << 16);
+  }
+  // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16).
+  __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
+    const int r = lane & 15, b = 4 * h + (lane >> 4);
+    const int src = (((r & 7) << 3) + b) << 2;
+    const uint32_t va[4] = {qa.x, qa.y, qa.z, qa.w}, vb[4] = {qb.x, qb.y, qb.z, qb.w};
+    uint32_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t x0 = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(va[j])));
+      const uint32_t x1 = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(vb[j])));
+      q[j] = (r & 8) ? x1 : x0;
+    }
+    out.q = make_uint4(q[0], q[1], q[2], q[3]);
+    const uint32_t dv = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(((r << 2) + (b >> 1)) << 2, static_cast<int>(dd)));
+    out.d = (b & 1) ? dv >> 16 : dv & 0xffffu;
+  }
+};
+
+// Routing shared by both forms: the expert's pairs as [begin, end) of lst.
+// Fused (offsets == nullptr): scan ids into s_list; expert 0's workgroups
+// also clear the rows of pairs routed nowhere over columns [c0, c1).
+template <bool F32_OUT>
+__device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
+                                          int64_t e, const int32_t* __restrict__ offsets,
+                                          const int32_t* __restrict__ list, int32_t* s_list, int32_t& s_n,
+                                          void* __restrict__ y, int64_t n_rows, int64_t c0, int64_t c1, int tid,
+                                          int nthreads, int32_t& begin, int32_t& end, const int32_t*& lst) {
+  if (offsets == nullptr) {
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    for (int32_t p = tid; p < n_pairs; p += nthreads) {
+      const int32_t id = ids[p];
+      if (id == e) s_list[atomicAdd(&s_n, 1)] = p;
+      if (e == 0 && (id < 0 || id >= n_expert)) {
+        for (int64_t c = c0; c < min(c1, n_rows); ++c) {
+          if constexpr (F32_OUT)
+            static_cast<float*>(y)[p * n_rows + c] = 0.0f;
+          else
+            static_cast<uint16_t*>(y)[p * n_rows + c] = 0;
+        }
+      }
+    }
+    __syncthreads();
+    begin = 0;
+    end = s_n;
+    lst = s_list;
+  } else {
+    begin = offsets[e];
+    end = offsets[e + 1];
+    lst = list;
+  }
+}
+
+template <int TYPE, bool F32_OUT>
+__global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
+    const uint8_t* __restrict__ w, int64_t expert_stride, int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
+    int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
+    int64_t rows_per_wg) {
+  extern __shared__ __align__(16) uint16_t As[];  // kMoeTok rows of `pitch` bf16
+  __shared__ int32_t s_pair[kMoeTok];
+  __shared__ int64_t s_xrow[kMoeTok];
+  __shared__ int32_t s_list[kFusedPairs];
+  __shared__ int32_t s_n;
+  constexpr int R = kStreamRing<TYPE>;
+  const int64_t e = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
+  const int64_t r1 = min(r0 + rows_per_wg, n_rows);
+  int32_t begin, end;
+  const int32_t* lst;
+  moe_route<F32_OUT>(ids, n_pairs, n_expert, e, offsets, list, s_list, s_n, y, n_rows, r0, r1, tid, kStreamThreads,
+                     begin, end, lst);
+  if (begin >= end || r0 >= r1) return;
+
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4;
+  const int64_t nb = k / block_elems(TYPE);
+  const int64_t steps = (k + 127) / 128;
+  const int pitch = static_cast<int>(steps * 128 + 8);
+  const Planes P = make_planes<TYPE>(w + e * expert_stride, n_rows, nb);
+  // This wave's groups: ordinals j = 0 .. my_groups - 1, group wave + 8 j.
+  const int64_t groups = (r1 - r0 + 15) / 16;
+  const int64_t my_groups = groups > wave ? (groups - wave + 7) / 8 : 0;
+  const int64_t units = (steps + Unit<TYPE>::kSteps - 1) / Unit<TYPE>::kSteps;
+  const bool ragged = k % 128 != 0;
+  const auto row_of = [&](int64_t j) { return r0 + 16 * (wave + 8 * j) + (lane & 15); };
+
+  for (int32_t t0 = begin; t0 < end; t0 += kMoeTok) {
+    const int nt = min(kMoeTok, end - t0);
+    __syncthreads();
+    if (tid < kMoeTok) {
+      const int32_t pr = tid < nt ? lst[t0 + tid] : -1;
+      s_pair[tid] = pr;
+      if (pr >= 0) {
+        const int64_t t = pr / top_k, slot = pr % top_k;
+        s_xrow[tid] = (t * x_slots + slot % x_slots) * k;
+      }
+    }
+    // Weights do not depend on the tokens: fill the ring first. Load
+    // pointer: unit (lj, lu) = (group ordinal, unit of the group); units
+    // past the wave's last are not loaded.
+    using U = Unit<TYPE>;
+    U ring[R];
+    int64_t lj = 0, lu = 0;
+    typename U::Addr la = U::addr(row_of(0) - (lane & 15), n_rows, nb, lane);
+#pragma unroll
+    for (int i = 0; i < R - 1; ++i) {
+      if (lj < my_groups) ring[i].load(P, la, lu, nb);
+      if (++lu == units) {
+        lu = 0;
+        ++lj;
+        la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
+      }
+    }
+    __syncthreads();
+    moe_stage<TYPE>(As, x, s_xrow, nt, k, 0, tid, static_cast<int>(steps * 128), pitch, kStreamThreads);
+    __syncthreads();
+
+    // MFMA rows past nt read row nt - 1; their outputs are dropped.
+    const uint16_t* arow = As + min(lane & 15, nt - 1) * pitch + 8 * g;
+    f32x4_t acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    int64_t cj = 0, cu = 0;  // compute pointer
+    const int64_t n_units = my_groups * units;
+    for (int64_t i0 = 0; i0 < n_units; i0 += R) {
+#pragma unroll
+      for (int d = 0; d < R; ++d) {
+        if (i0 + d >= n_units) break;
+        if (lj < my_groups) ring[(d + R - 1) % R].load(P, la, lu, nb);
+        if (++lu == units) {
+          lu = 0;
+          ++lj;
+          la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
+        }
+#pragma unroll
+        for (int h = 0; h < U::kSteps; ++h) {
+          const int64_t st = cu * U::kSteps + h;
+          if (U::kSteps == 1 || st < steps) {
+            MoePiece<TYPE> pc;
+            ring[d].piece(pc, h, lane);
+            if constexpr (TYPE != SPIRAL_TYPE_Q4_0 && TYPE != SPIRAL_TYPE_Q6_K) {
+              // k tail: blocks past k read as zero
+              if (ragged && st == steps - 1 && 32 * (4 * st + g) >= k) pc.zero();
+            }
+            pc.prep();
+            const uint16_t* ak = arow + 8 * 16 * st;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const bf16x8_t b = __builtin_bit_cast(bf16x8_t, pc.dequant(s));
+              const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ak + 8 * 4 * s);
+              acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[s], 0, 0, 0);
+            }
+          }
+        }
+        if (++cu == units) {
+          // acc: lane l holds rows 4 (l / 16) + i (routed pairs) of column l % 16.
+          const int64_t n = row_of(cj);
+          const f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int32_t pr = s_pair[4 * g + i];
+            if (pr >= 0 && n < r1) {
+              if constexpr (F32_OUT)
+                static_cast<float*>(y)[pr * n_rows + n] = sum[i];
+              else
+                static_cast<__bf16*>(y)[pr * n_rows + n] = static_cast<__bf16>(sum[i]);
+            }
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          cu = 0;
+          ++cj;
+        }
+      }
+    }
+  }
+}
+
+// Dynamic LDS of the streaming form for k (0 when it does not fit).
+int64_t stream_lds_bytes(int64_t k) {
+  if (k > kStreamMaxK) return 0;
+  return kMoeTok * (((k + 127) / 128) * 128 + 8) * 2;
+}
+
+template <int TYPE, bool F32_OUT>
+int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
+                  const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
+                  const int32_t* offsets, const int32_t* list, void* y, hipStream_t s) {
+  const auto kern = moe_stream_kernel<TYPE, F32_OUT>;
+  const int64_t lds = stream_lds_bytes(k);
+  static bool attr_set = false;  // benign race: every caller sets the same value
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(stream_lds_bytes(kStreamMaxK))) != hipSuccess) {
+      (void)hipGetLastError();
+      return SPIRAL_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  // About two workgroups per CU in all, each over a contiguous range of
+  // whole 16-row groups of one expert.
+  const int64_t per_expert = std::max<int64_t>(1, ceil_div(2 * device_cu_count(), n_expert));
+  const int64_t rows_per_wg = ceil_div(ceil_div(n_rows, per_expert), 16) * 16;
+  const dim3 grid(static_cast<unsigned>(ceil_div(n_rows, rows_per_wg)), static_cast<unsigned>(n_expert));
+  hipLaunchKernelGGL(kern, grid, dim3(kStreamThreads), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
+                     expert_stride, n_rows, k, x, x_slots, top_k, ids, static_cast<int32_t>(n_pairs),
+                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg);
+  return launch_status();
+}
+
 }  // namespace
 
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_expert + 1 + n_pairs); }
@@ -591,6 +938,17 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
     hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
                        static_cast<int32_t>(n_expert), offsets, list, y, n_rows, f32);
     if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
+  }
+  if (stream_lds_bytes(k) > 0) {
+#define SPIRAL_MOE_STREAM(T)                                                                                 \
+  return f32 ? launch_stream<T, true>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, \
+                                      offsets, list, y, s)                                                    \
+             : launch_stream<T, false>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, \
+                                       offsets, list, y, s)
+    if (type == SPIRAL_TYPE_Q4_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q4_0);
+    if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q8_0);
+    SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q6_K);
+#undef SPIRAL_MOE_STREAM
   }
   const dim3 grid(static_cast<unsigned>(ceil_div(n_rows, kMoeBN)), static_cast<unsigned>(n_expert));
   const uint8_t* W = static_cast<const uint8_t*>(w);
