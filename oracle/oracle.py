@@ -58,6 +58,10 @@ def lib():
         L.oq_check_split_identity.restype = _i64
         L.oq_dequant.argtypes = [ctypes.c_int, _p, _i64, _i64, _i64, _p, _i64]
         L.oq_dequant.restype = ctypes.c_int
+        L.oq_dequant_f64.argtypes = [ctypes.c_int, _p, _i64, _i64, _i64, _p, _i64]
+        L.oq_dequant_f64.restype = ctypes.c_int
+        L.oq_matmul_f64_exact.argtypes = [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64]
+        L.oq_matmul_f64_exact.restype = None
         L.oq_get_rows.argtypes = [ctypes.c_int, _p, _i64, _i64, _i64, _p, _i64, _p, _i64]
         L.oq_get_rows.restype = ctypes.c_int
         L.oq_ref_record_count.argtypes = [ctypes.c_int, _i64, _i64]
@@ -106,6 +110,18 @@ def dequant(qtype, raw, n_rows, k, row_stride=None):
     rc = lib().oq_dequant(qtype, _ptr(raw), row_stride, n_rows, k, _ptr(out), k)
     if rc != 0:
         raise ValueError("oracle dequant: bad shape")
+    return out
+
+
+def dequant_exact(qtype, raw, n_rows, k, row_stride=None):
+    """Canonical rows -> the exact weights (float64, shape [n_rows, k]) that
+    dequant rounds to bf16 once."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    row_stride = row_bytes(qtype, k) if row_stride is None else row_stride
+    out = np.empty((n_rows, k), dtype=np.float64)
+    rc = lib().oq_dequant_f64(qtype, _ptr(raw), row_stride, n_rows, k, _ptr(out), k)
+    if rc != 0:
+        raise ValueError("oracle dequant_exact: bad shape")
     return out
 
 
@@ -166,6 +182,17 @@ def matmul_f64(w_bf16, x_bf16):
     m = x.shape[0]
     y = np.empty((m, n), dtype=np.float64)
     lib().oq_matmul_f64(_ptr(w), k, n, k, _ptr(x), k, m, _ptr(y), n)
+    return y
+
+
+def matmul_f64_exact(w_f64, x_bf16):
+    """y[m, n] = sum_k x[m, k] * w[n, k] in float64 over float64 weights."""
+    w = np.ascontiguousarray(w_f64, dtype=np.float64)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    n, k = w.shape
+    m = x.shape[0]
+    y = np.empty((m, n), dtype=np.float64)
+    lib().oq_matmul_f64_exact(_ptr(w), k, n, k, _ptr(x), k, m, _ptr(y), n)
     return y
 
 

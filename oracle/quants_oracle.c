@@ -198,21 +198,24 @@ int oq_block_elems(int type) {
   }
 }
 
-static void dequant_block(int type, const uint8_t* blk, uint16_t* y) {
+/* Exact values of one block's weights. Every product below is exact in
+ * float (Q4_0 <= 15, Q8_0 <= 19, Q6_K <= 23 significant bits), so rounding
+ * these to bf16 is the format's single rounding. */
+static void dequant_block_exact(int type, const uint8_t* blk, double* y) {
   if (type == OQ_Q4_0) {
     /* src/quants/tests/formats/q4_0.py:53-60: low nibbles are elements 0..15,
      * high nibbles 16..31, value (q - 8) * d. */
     const float d = oq_fp16_device(le16(blk));
     const uint8_t* qs = blk + 2;
     for (int j = 0; j < 16; ++j) {
-      y[j] = oq_bf16_rne((float)((qs[j] & 15) - 8) * d);
-      y[j + 16] = oq_bf16_rne((float)((qs[j] >> 4) - 8) * d);
+      y[j] = (double)((qs[j] & 15) - 8) * d;
+      y[j + 16] = (double)((qs[j] >> 4) - 8) * d;
     }
   } else if (type == OQ_Q8_0) {
     /* src/quants/tests/formats/q8_0.py:50-58: int8 code times d. */
     const float d = oq_fp16_device(le16(blk));
     const int8_t* qs = (const int8_t*)(blk + 2);
-    for (int j = 0; j < 32; ++j) y[j] = oq_bf16_rne((float)qs[j] * d);
+    for (int j = 0; j < 32; ++j) y[j] = (double)qs[j] * d;
   } else {
     /* src/quants/tests/formats/q6_k.py:55-97: ql[128] qh[64] sc[16] d. */
     const uint8_t* ql = blk;
@@ -230,12 +233,19 @@ static void dequant_block(int type, const uint8_t* blk, uint16_t* y) {
             (lo1 >> 4) | (((hb >> 6) & 3) << 4),
         };
         for (int j = 0; j < 4; ++j) {
-          const float ds = d * (float)sc[8 * h + l / 16 + 2 * j];
-          y[128 * h + 32 * j + l] = oq_bf16_rne(ds * (float)(q[j] - 32));
+          const double ds = (double)d * (double)sc[8 * h + l / 16 + 2 * j];
+          y[128 * h + 32 * j + l] = ds * (double)(q[j] - 32);
         }
       }
     }
   }
+}
+
+static void dequant_block(int type, const uint8_t* blk, uint16_t* y) {
+  double v[256];
+  dequant_block_exact(type, blk, v);
+  const int be = oq_block_elems(type);
+  for (int j = 0; j < be; ++j) y[j] = oq_bf16_rne((float)v[j]);
 }
 
 static int shape_ok(int type, int64_t n_rows, int64_t k) {
@@ -255,6 +265,33 @@ int oq_dequant(int type, const uint8_t* src, int64_t row_stride,
     }
   }
   return 0;
+}
+
+int oq_dequant_f64(int type, const uint8_t* src, int64_t row_stride,
+                   int64_t n_rows, int64_t k, double* out, int64_t ld_out) {
+  if (!shape_ok(type, n_rows, k)) return -1;
+  const int be = oq_block_elems(type), bb = oq_block_bytes(type);
+  const int64_t nb = k / be;
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < n_rows; ++n) {
+    for (int64_t b = 0; b < nb; ++b) {
+      dequant_block_exact(type, src + n * row_stride + b * bb, out + n * ld_out + b * be);
+    }
+  }
+  return 0;
+}
+
+void oq_matmul_f64_exact(const double* w, int64_t ldw, int64_t n_rows, int64_t k,
+                         const uint16_t* x, int64_t ldx, int64_t m, double* y,
+                         int64_t ldy) {
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < n_rows; ++n) {
+    for (int64_t i = 0; i < m; ++i) {
+      double acc = 0.0;
+      for (int64_t kk = 0; kk < k; ++kk) acc += w[n * ldw + kk] * (double)oq_bf16_f32(x[i * ldx + kk]);
+      y[i * ldy + n] = acc;
+    }
+  }
 }
 
 int oq_get_rows(int type, const uint8_t* src, int64_t row_stride,

@@ -96,6 +96,14 @@ int oq_dequant(int type, const uint8_t* src, int64_t row_stride,
                int64_t n_rows, int64_t k, uint16_t* out, int64_t ld_out);
 
 /* Dequantize selected rows (ggml GET_ROWS) into row-major bf16. */
+/* Canonical rows -> the exact (unrounded) weights as double: the values
+ * that oq_dequant rounds to bf16 once. */
+int oq_dequant_f64(int type, const uint8_t* src, int64_t row_stride,
+                   int64_t n_rows, int64_t k, double* out, int64_t ld_out);
+/* y[m, n] = sum_k x[m, k] * w[n, k] in double over double weights. */
+void oq_matmul_f64_exact(const double* w, int64_t ldw, int64_t n_rows, int64_t k,
+                         const uint16_t* x, int64_t ldx, int64_t m, double* y,
+                         int64_t ldy);
 int oq_get_rows(int type, const uint8_t* src, int64_t row_stride,
                 int64_t n_rows, int64_t k, const int32_t* ids, int64_t n_ids,
                 uint16_t* out, int64_t ld_out);

@@ -226,9 +226,11 @@ template <>
 struct MoePiece<SPIRAL_TYPE_Q6_K> {
   uint4 l0, l1, h0, h1;
   uint32_t ds2;  // fp16 d (bits 0..15), sc for l < 16 (16..23), sc for l >= 16 (24..31)
+  uint32_t sch;  // or-ed into ds2 bits 16..31 by prep (the streaming form loads it apart)
   int ls, hs;
   float m0, off0, m1, off1;  // d * sc and offsets for l < 16 and l >= 16 (prep)
   __device__ __forceinline__ void prep() {
+    ds2 |= sch << 16;
     const float d = fp16_scale(ds2 & 0xffffu);
     m0 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 16));
     m1 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 24));
@@ -246,10 +248,11 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
     h1 = *reinterpret_cast<const uint4*>(qh + 16);
     const uint32_t sc = *reinterpret_cast<const uint16_t*>(we + tot * 192 + sbi * 16 + 8 * h + 2 * g);
     ds2 = *reinterpret_cast<const uint16_t*>(we + tot * 208 + sbi * 2) | (sc << 16);
+    sch = 0u;
     ls = (g >> 1) * 4;
     hs = 2 * g;
   }
-  __device__ __forceinline__ void zero() { l0 = l1 = h0 = h1 = make_uint4(0u, 0u, 0u, 0u); ds2 = 0u; ls = hs = 0; }
+  __device__ __forceinline__ void zero() { l0 = l1 = h0 = h1 = make_uint4(0u, 0u, 0u, 0u); ds2 = sch = 0u; ls = hs = 0; }
   __device__ __forceinline__ uint4 dequant(int s) const {
     const uint4 L = s < 2 ? l0 : l1, H = s < 2 ? h0 : h1;
     const uint32_t wl0 = (s & 1) ? L.z : L.x, wl1 = (s & 1) ? L.w : L.y;
@@ -413,6 +416,7 @@ struct WStage<SPIRAL_TYPE_Q6_K> {
     pc.h1 = *reinterpret_cast<const uint4*>(qh + 16);
     const uint32_t sc = *reinterpret_cast<const uint16_t*>(st + kScOff + r * 16 + 8 * h + 2 * g);
     pc.ds2 = *reinterpret_cast<const uint16_t*>(st + kDOff + r * 2) | (sc << 16);
+    pc.sch = 0u;
     pc.ls = (g >> 1) * 4;
     pc.hs = 2 * g;
   }
@@ -648,8 +652,8 @@ struct PieceAddr<SPIRAL_TYPE_Q6_K> {
     pc.l1 = bload16(P.a, l + 16u, sb * 128u + 64u * hh);
     pc.h0 = bload16(P.b, h, sb * 64u + 32u * hh);
     pc.h1 = bload16(P.b, h + 16u, sb * 64u + 32u * hh);
-    const uint32_t scv = bload2(P.c, sc, sb * 16u + 8u * hh);
-    pc.ds2 = bload2(P.d, d, sb * 2u) | (scv << 16);
+    pc.sch = bload2(P.c, sc, sb * 16u + 8u * hh);
+    pc.ds2 = bload2(P.d, d, sb * 2u);
     pc.ls = (g >> 1) * 4;
     pc.hs = 2 * g;
   }
@@ -681,8 +685,8 @@ struct Unit {
 template <>
 struct Unit<SPIRAL_TYPE_Q4_0> {
   static constexpr int kSteps = 2;
-  uint4 qa, qb;  // rows lane / 8 and 8 + lane / 8 of the group, block 8 u + lane % 8
-  uint32_t dd;   // row lane / 4: d of blocks 8 u + 2 (lane % 4) (low half) and + 1
+  uint4 qa, qb;    // rows lane / 8 and 8 + lane / 8 of the group, block 8 u + lane % 8
+  uint32_t d0, d1;  // row lane / 4: d of blocks 8 u + 2 (lane % 4) and + 1
   struct Addr {
     uint32_t qa, qb, d;
     int c, dc;
@@ -696,15 +700,19 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
     a.d = static_cast<uint32_t>((min(row0 + (lane >> 2), n_rows - 1) * nb + a.dc) * 2);
     return a;
   }
+  // Every load is issued (a load under a branch, or a value combined from
+  // loads here, makes the compiler wait for the ring's loads at once).
+  // Blocks past nb read d = 0 through an offset past the buffer's range, so
+  // their pieces are zero whatever their codes (the next row's bytes, or
+  // zero past the plane).
   __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t nb) {
     const int64_t b = 8 * u;
     const uint32_t sq = static_cast<uint32_t>(b * 16), sd = static_cast<uint32_t>(b * 2);
-    const bool qv = b + a.c < nb;
-    qa = qv ? bload16(P.a, a.qa, sq) : make_uint4(0u, 0u, 0u, 0u);
-    qb = qv ? bload16(P.a, a.qb, sq) : make_uint4(0u, 0u, 0u, 0u);
-    const uint32_t d0 = b + a.dc < nb ? bload2(P.d, a.d, sd) : 0u;
-    const uint32_t d1 = b + a.dc + 1 < nb ? bload2(P.d, a.d + 2, sd) : 0u;
-    dd = d0 | (d1 << 16);
+    constexpr uint32_t kOut = 0x80000000u;  // beyond every plane (experts are < 2 GiB)
+    qa = bload16(P.a, a.qa, sq);
+    qb = bload16(P.a, a.qb, sq);
+    d0 = bload2(P.d, b + a.dc < nb ? a.d + sd : kOut, 0u);
+    d1 = bload2(P.d, b + a.dc + 1 < nb ? a.d + 2 + sd : kOut, 0u);
   }
   // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16).
   __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
@@ -719,6 +727,7 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
       q[j] = (r & 8) ? x1 : x0;
     }
     out.q = make_uint4(q[0], q[1], q[2], q[3]);
+    const uint32_t dd = d0 | (d1 << 16);
     const uint32_t dv = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(((r << 2) + (b >> 1)) << 2, static_cast<int>(dd)));
     out.d = (b & 1) ? dv >> 16 : dv & 0xffffu;
   }
@@ -806,21 +815,25 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
       }
     }
     // Weights do not depend on the tokens: fill the ring first. Load
-    // pointer: unit (lj, lu) = (group ordinal, unit of the group); units
-    // past the wave's last are not loaded.
+    // pointer: unit (lj, lu) = (group ordinal, unit of the group). Every
+    // ring load is issued, so the compiler can count the loads in flight
+    // and wait for exactly the one it needs (a load under a branch makes it
+    // wait for all of them); past the wave's last unit the ring re-reads it.
     using U = Unit<TYPE>;
     U ring[R];
-    int64_t lj = 0, lu = 0;
+    const int n_units = static_cast<int>(my_groups * units);
+    int lj = 0, lu = 0, nl = 0;
     typename U::Addr la = U::addr(row_of(0) - (lane & 15), n_rows, nb, lane);
-#pragma unroll
-    for (int i = 0; i < R - 1; ++i) {
-      if (lj < my_groups) ring[i].load(P, la, lu, nb);
-      if (++lu == units) {
+    const auto issue = [&](int slot) {
+      ring[slot].load(P, la, lu, nb);
+      if (++nl < n_units && ++lu == units) {
         lu = 0;
         ++lj;
         la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
       }
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < R - 1; ++i) issue(i);
     __syncthreads();
     moe_stage<TYPE>(As, x, s_xrow, nt, k, 0, tid, static_cast<int>(steps * 128), pitch, kStreamThreads);
     __syncthreads();
@@ -830,60 +843,64 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     f32x4_t acc[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    int64_t cj = 0, cu = 0;  // compute pointer
-    const int64_t n_units = my_groups * units;
-    for (int64_t i0 = 0; i0 < n_units; i0 += R) {
+    int cj = 0, cu = 0;  // compute pointer
+    const auto compute = [&](int slot) {
 #pragma unroll
-      for (int d = 0; d < R; ++d) {
-        if (i0 + d >= n_units) break;
-        if (lj < my_groups) ring[(d + R - 1) % R].load(P, la, lu, nb);
-        if (++lu == units) {
-          lu = 0;
-          ++lj;
-          la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
-        }
-#pragma unroll
-        for (int h = 0; h < U::kSteps; ++h) {
-          const int64_t st = cu * U::kSteps + h;
-          if (U::kSteps == 1 || st < steps) {
-            MoePiece<TYPE> pc;
-            ring[d].piece(pc, h, lane);
-            if constexpr (TYPE != SPIRAL_TYPE_Q4_0 && TYPE != SPIRAL_TYPE_Q6_K) {
-              // k tail: blocks past k read as zero
-              if (ragged && st == steps - 1 && 32 * (4 * st + g) >= k) pc.zero();
-            }
-            pc.prep();
-            const uint16_t* ak = arow + 8 * 16 * st;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const bf16x8_t b = __builtin_bit_cast(bf16x8_t, pc.dequant(s));
-              const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ak + 8 * 4 * s);
-              acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[s], 0, 0, 0);
-            }
+      for (int h = 0; h < U::kSteps; ++h) {
+        const int64_t st = static_cast<int64_t>(cu) * U::kSteps + h;
+        if (U::kSteps == 1 || st < steps) {
+          MoePiece<TYPE> pc;
+          ring[slot].piece(pc, h, lane);
+          if constexpr (TYPE != SPIRAL_TYPE_Q4_0 && TYPE != SPIRAL_TYPE_Q6_K) {
+            // k tail: blocks past k read as zero
+            if (ragged && st == steps - 1 && 32 * (4 * st + g) >= k) pc.zero();
           }
-        }
-        if (++cu == units) {
-          // acc: lane l holds rows 4 (l / 16) + i (routed pairs) of column l % 16.
-          const int64_t n = row_of(cj);
-          const f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+          pc.prep();
+          const uint16_t* ak = arow + 8 * 16 * st;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int32_t pr = s_pair[4 * g + i];
-            if (pr >= 0 && n < r1) {
-              if constexpr (F32_OUT)
-                static_cast<float*>(y)[pr * n_rows + n] = sum[i];
-              else
-                static_cast<__bf16*>(y)[pr * n_rows + n] = static_cast<__bf16>(sum[i]);
-            }
+          for (int s = 0; s < 4; ++s) {
+            const bf16x8_t b = __builtin_bit_cast(bf16x8_t, pc.dequant(s));
+            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ak + 8 * 4 * s);
+            acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[s], 0, 0, 0);
           }
-#pragma unroll
-          for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-          cu = 0;
-          ++cj;
         }
       }
+      if (++cu == units) {
+        // acc: lane l holds rows 4 (l / 16) + i (routed pairs) of column l % 16.
+        const int64_t n = row_of(cj);
+        const f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int32_t pr = s_pair[4 * g + i];
+          if (pr >= 0 && n < r1) {
+            if constexpr (F32_OUT)
+              static_cast<float*>(y)[pr * n_rows + n] = sum[i];
+            else
+              static_cast<__bf16*>(y)[pr * n_rows + n] = static_cast<__bf16>(sum[i]);
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        cu = 0;
+        ++cj;
+      }
+    };
+    // Whole rounds of R units (each issues the load R - 1 units ahead), then
+    // the last units, which are already in the ring.
+    int i0 = 0;
+    for (; i0 + R <= n_units; i0 += R) {
+#pragma unroll
+      for (int d = 0; d < R; ++d) {
+        issue((d + R - 1) % R);
+        compute(d);
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < R - 1; ++d) {
+      if (i0 + d < n_units) compute(d);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // the ring's last (repeated) loads
 }
 
 // Dynamic LDS of the streaming form for k (0 when it does not fit).

@@ -9,6 +9,8 @@ Each oracle function is checked by something other than its own formula:
     hand-computed golden blocks (tests/golden/special_blocks.json);
   - record layout: the reference's own repack.h compiled into oracle/_ref, and
     fixtures made from it (tests/golden/ref_records.npz);
+  - exact (unrounded) weights: exact fractions, a numpy restatement of Q4_0,
+    and rounding them once to bf16 gives dequant's bits;
   - matmul: numpy float64.
 """
 
@@ -137,7 +139,7 @@ def _bf16_of_fraction(v):
     return int(torch.from_numpy(f).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[0])
 
 
-def _exact_block(qtype, blk):
+def _exact_values(qtype, blk):
     """Element values of one canonical block, written from the format
     description (src/quants/tests/formats/*.py) with exact fractions."""
     out = []
@@ -160,7 +162,11 @@ def _exact_block(qtype, blk):
             nib = (byte >> 4) if j >= 2 else (byte & 15)
             q = nib | (((qh[32 * h + l] >> (2 * j)) & 3) << 4)
             out[e] = d * sc[8 * h + l // 16 + 2 * j] * (q - 32)
-    return [_bf16_of_fraction(v) for v in out]
+    return out
+
+
+def _exact_block(qtype, blk):
+    return [_bf16_of_fraction(v) for v in _exact_values(qtype, blk)]
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
@@ -185,6 +191,45 @@ def test_dequant_matches_exact_arithmetic(oracle, qtype):
     # zero results may differ only in sign (see test_q_times_d_exhaustive)
     both_zero = ((got & 0x7FFF) == 0) & ((want & 0x7FFF) == 0)
     assert np.array_equal(np.where(both_zero, 0, got), np.where(both_zero, 0, want))
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_dequant_exact_matches_fractions_and_rounds_to_dequant(oracle, qtype):
+    """The unrounded weights: equal to the exact rational values, and their
+    one rounding to bf16 is dequant's output."""
+    rng = np.random.default_rng(100 + qtype)
+    k = O.BLOCK_ELEMS[qtype] * 3
+    n = 4
+    raw = rng.integers(0, 256, n * O.row_bytes(qtype, k), dtype=np.uint8)
+    blocks = raw.reshape(-1, O.BLOCK_BYTES[qtype])
+    dpos = 0 if qtype != O.Q6_K else 208
+    dbits = rng.integers(0, 0x7C00, blocks.shape[0]).astype(np.uint16) | (
+        rng.integers(0, 2, blocks.shape[0]).astype(np.uint16) << 15)
+    dbits[0] = 0x0123   # subnormal -> +0
+    dbits[1] = 0x7C05   # exponent 31 -> finite
+    blocks[:, dpos] = dbits & 0xFF
+    blocks[:, dpos + 1] = dbits >> 8
+    got = O.dequant_exact(qtype, raw, n, k)
+    want = [v for b in blocks for v in _exact_values(qtype, b)]
+    assert all(Fraction(float(g)) == w for g, w in zip(got.reshape(-1), want))
+    rounded = O.bf16_rne(got.astype(np.float32))
+    bits16 = O.dequant(qtype, raw, n, k)
+    both_zero = ((rounded & 0x7FFF) == 0) & ((bits16 & 0x7FFF) == 0)
+    assert np.array_equal(np.where(both_zero, 0, rounded), np.where(both_zero, 0, bits16))
+
+
+def test_dequant_exact_q4_0_numpy_restatement(oracle):
+    """Q4_0 from its bytes with numpy alone: (nibble - 8) * d."""
+    rng = np.random.default_rng(7)
+    n, k = 5, 128
+    raw = rng.integers(0, 256, n * O.row_bytes(O.Q4_0, k), dtype=np.uint8)
+    blocks = raw.reshape(-1, 18)
+    blocks[:, 1] &= 0x7B  # normal, finite scales
+    blocks[:, 1] |= 0x04
+    d = blocks[:, :2].copy().view(np.float16).astype(np.float64)[:, 0]
+    qs = blocks[:, 2:].astype(np.int64)
+    vals = np.concatenate([(qs & 15) - 8, (qs >> 4) - 8], axis=1) * d[:, None]
+    assert np.array_equal(O.dequant_exact(O.Q4_0, raw, n, k), vals.reshape(n, k))
 
 
 def test_golden_special_blocks(oracle):
@@ -272,6 +317,14 @@ def test_matmul_f64_matches_numpy(oracle):
     xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
     assert np.allclose(O.matmul_f64(w, x), xf @ wf.T, rtol=1e-12, atol=1e-12)
     assert np.allclose(O.matmul_f32(w, x), xf @ wf.T, rtol=1e-5, atol=1e-4)
+
+
+def test_matmul_f64_exact_matches_numpy(oracle):
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((33, 64))
+    x = O.bf16_rne(rng.standard_normal((6, 64)).astype(np.float32))
+    xf = (x.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    assert np.allclose(O.matmul_f64_exact(w, x), xf @ w.T, rtol=1e-12, atol=1e-12)
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
