@@ -6,7 +6,7 @@
 
 Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
 x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
-workloads under "workloads": Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
+workloads under "workloads": Q4_0 GEMV (14336 x 4096), Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
 and Q6_K -> bf16 dequant (4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096) and the Q4_0 MoE
 grouped GEMM (128 experts, 64 tokens, top-8).
 
@@ -120,7 +120,7 @@ def traffic_table():
 TRAFFIC_KERNELS = {
     "gemv_q8_0": (["gemv_kernel<8,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
     "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
-    "gemv_q4_0": (["gemv_kernel<2,"], 4096 * 4096 // 32 * 18 + 4096 * 2 + 4096 * 2),
+    "gemv_q4_0": (["gemv_kernel<2,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
@@ -264,16 +264,16 @@ def main():
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
 
-    # --- Q4_0 GEMV ------------------------------------------------------------
+    # --- Q4_0 GEMV (the FFN up/gate shape of the Q8_0 workload) --------------------
     if want("gemv_q4_0"):
-        n, k = 4096, 4096
+        n, k = 14336, 4096
         wbytes = n * row_bytes(TYPE_Q4_0, k)
         _, ws = upload_planar(TYPE_Q4_0, n, k, 5, copies_for(wbytes))
         _, xd = x_dev(1, k, 6)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
         wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
         record("gemv_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
-               {"workload": "Q4_0 decode GEMV y[4096] = W[4096x4096] x[4096], batch 1, bf16 out",
+               {"workload": "Q4_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
 

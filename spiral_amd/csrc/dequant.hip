@@ -19,24 +19,34 @@
 namespace spiral {
 namespace {
 
-// A workgroup covers 256 groups of 8 elements of one row; row and group
-// come from the workgroup index with one 32-bit scalar division, so no
-// thread divides.
+// A workgroup covers kDequantGroups groups of 8 elements of one row; row and
+// group come from the workgroup index with one 32-bit scalar division, so no
+// thread divides. Each thread converts two groups 256 apart (both loads
+// issued before either is used), so each store instruction of a wave still
+// writes 1 KiB of consecutive bytes.
+constexpr int kDequantGroups = 512;
 template <int TYPE>
 __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
                                                       int64_t nb, uint32_t groups_per_row, uint32_t wg_per_row,
                                                       uint16_t* __restrict__ out, int64_t ld_out) {
   const uint32_t row = blockIdx.x / wg_per_row;
-  const uint32_t g = (blockIdx.x - row * wg_per_row) * 256 + threadIdx.x;
-  if (g >= groups_per_row) return;
-  float v[8];
-  dequant8<TYPE>(w, n_rows, nb, row, g, v);
-  uint4 o;
-  o.x = pack_bf16x2(v[0], v[1]);
-  o.y = pack_bf16x2(v[2], v[3]);
-  o.z = pack_bf16x2(v[4], v[5]);
-  o.w = pack_bf16x2(v[6], v[7]);
-  *reinterpret_cast<uint4*>(out + row * ld_out + 8 * g) = o;
+  const uint32_t g0 = (blockIdx.x - row * wg_per_row) * kDequantGroups + threadIdx.x;
+  if (g0 >= groups_per_row) return;
+  const uint32_t g1 = g0 + 256;
+  const bool second = g1 < groups_per_row;
+  float v[2][8];
+  dequant8<TYPE>(w, n_rows, nb, row, g0, v[0]);
+  dequant8<TYPE>(w, n_rows, nb, row, second ? g1 : g0, v[1]);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h == 1 && !second) break;
+    uint4 o;
+    o.x = pack_bf16x2(v[h][0], v[h][1]);
+    o.y = pack_bf16x2(v[h][2], v[h][3]);
+    o.z = pack_bf16x2(v[h][4], v[h][5]);
+    o.w = pack_bf16x2(v[h][6], v[h][7]);
+    *reinterpret_cast<uint4*>(out + row * ld_out + 8 * (h ? g1 : g0)) = o;
+  }
 }
 
 template <int TYPE, bool F32_OUT>
@@ -85,8 +95,8 @@ int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k, uint
   if (!aligned16(w) || !aligned16(out) || ld_out % 8 != 0) return SPIRAL_ERR_ALIGN;
   int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
-  const int64_t nb = k / block_elems(type), gpr = k / 8, wpr = ceil_div(gpr, 256);
-  if (gpr > UINT32_MAX || n_rows > UINT32_MAX || n_rows * wpr > UINT32_MAX) return SPIRAL_ERR_SHAPE;
+  const int64_t nb = k / block_elems(type), gpr = k / 8, wpr = ceil_div(gpr, kDequantGroups);
+  if (gpr + 256 > UINT32_MAX || n_rows > UINT32_MAX || n_rows * wpr > UINT32_MAX) return SPIRAL_ERR_SHAPE;
   const dim3 grid(static_cast<unsigned>(n_rows * wpr));
   const uint32_t g32 = static_cast<uint32_t>(gpr), w32 = static_cast<uint32_t>(wpr);
   hipStream_t s = static_cast<hipStream_t>(stream);

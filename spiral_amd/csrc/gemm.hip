@@ -61,26 +61,41 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t grid) {
 }
 
 // Xp[mb][kk][lane][8] = X[16 mb + lane % 16][32 kk + 8 (lane / 16) + e];
-// rows past m are zero. Workgroup (mb, group of 16 kk): wave w writes the
-// four fragments kk = 16 g + 4 w .. + 3, four loads in flight per lane.
+// rows past m are zero. Workgroup (mb, group of 16 kk) packs a 16-row x
+// 512-column tile through LDS:
+//  - wave w reads rows 4 w .. + 3 of the tile, each as one 1 KiB load with
+//    consecutive lanes on consecutive 16 bytes of the row (reading the
+//    fragments straight from X puts consecutive lanes on different rows,
+//    which the gfx950 address path serves at about a third of the rate);
+//  - after a barrier, wave w writes fragments kk = 16 g + 4 w .. + 3, each a
+//    1 KiB store of consecutive bytes. Tile rows are padded by 16 bytes so
+//    the 16 rows a fragment reads land in different LDS banks.
+constexpr int kPackPitch = 512 + 8;  // bf16 per LDS tile row
 __global__ void __launch_bounds__(256) pack_x_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t m,
                                                      int64_t k, uint16_t* __restrict__ xp) {
+  __shared__ __align__(16) uint16_t tile[16 * kPackPitch];
   const uint32_t kk_n = static_cast<uint32_t>(k >> 5);
   const uint32_t groups = (kk_n + 15) >> 4;
   const uint32_t mb = blockIdx.x / groups, kg = blockIdx.x - mb * groups;
-  const uint32_t lane = threadIdx.x & 63u, kk0 = 16 * kg + 4 * (threadIdx.x >> 6);
-  const int64_t r = 16 * static_cast<int64_t>(mb) + (lane & 15);
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const int64_t col = 512 * static_cast<int64_t>(kg) + 8 * lane;  // this lane's 8 columns
   uint4 v[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
+    const int64_t r = 16 * static_cast<int64_t>(mb) + 4 * w + t;
     v[t] = make_uint4(0u, 0u, 0u, 0u);
-    if (r < m && kk0 + t < kk_n)
-      v[t] = *reinterpret_cast<const uint4*>(x + r * ldx + 32 * (kk0 + t) + 8 * (lane >> 4));
+    if (r < m && col < k) v[t] = *reinterpret_cast<const uint4*>(x + r * ldx + col);
   }
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
-    if (kk0 + t < kk_n)
-      *reinterpret_cast<uint4*>(xp + ((static_cast<int64_t>(mb) * kk_n + kk0 + t) * 64 + lane) * 8) = v[t];
+  for (int t = 0; t < 4; ++t) *reinterpret_cast<uint4*>(tile + (4 * w + t) * kPackPitch + 8 * lane) = v[t];
+  __syncthreads();
+  const uint32_t kk0 = 16 * kg + 4 * w;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (kk0 + t >= kk_n) break;
+    const uint4 f = *reinterpret_cast<const uint4*>(tile + (lane & 15) * kPackPitch + 32 * (4 * w + t) + 8 * (lane >> 4));
+    *reinterpret_cast<uint4*>(xp + ((static_cast<int64_t>(mb) * kk_n + kk0 + t) * 64 + lane) * 8) = f;
+  }
 }
 
 // The four X fragments (m-blocks) of a wave for one k-quarter.
