@@ -6,7 +6,8 @@
 
 Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
 x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
-workloads under "workloads": Q4_0 GEMV (14336 x 4096), Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
+workloads under "workloads": Q4_0 GEMV (14336 x 4096), the Q4_0 small-batch
+product at m = 4 (same matrix), Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
 and Q6_K -> bf16 dequant (4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096) and the Q4_0 MoE
 grouped GEMM (128 experts, 64 tokens, top-8).
 
@@ -121,6 +122,7 @@ TRAFFIC_KERNELS = {
     "gemv_q8_0": (["gemv_kernel<8,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
     "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
     "gemv_q4_0": (["gemv_kernel<2,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "mul_mat_q4_0_m4": (["skinny_kernel<2,"], 14336 * 4096 // 32 * 18 + 4 * 4096 * 2 + 4 * 14336 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
@@ -275,6 +277,21 @@ def main():
         record("gemv_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
+        del ws
+
+    # --- Q4_0 small-batch product, m = 4 (speculative-decode batch) ---------------
+    if want("mul_mat_q4_0_m4"):
+        m, n, k = 4, 14336, 4096
+        wbytes = n * row_bytes(TYPE_Q4_0, k)
+        step_bytes = wbytes + m * k * 2 + m * n * 2
+        _, ws = upload_planar(TYPE_Q4_0, n, k, 11, copies_for(wbytes))
+        _, xd = x_dev(m, k, 12)
+        y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("mul_mat_q4_0_m4", wall, ev, step_bytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q4_0 small-batch product Y[4x14336] = X[4x4096] W[14336x4096]^T, bf16 MFMA, "
+                            "fp32 acc, bf16 out",
+                "bytes_per_launch": step_bytes, "copies": len(ws)})
         del ws
 
     # --- Q4_0 -> bf16 dequant ---------------------------------------------------

@@ -150,12 +150,15 @@ int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k,
 
 /* ggml MUL_MAT with quantized src0: y[i][n] = sum_k x[i][k] * W[n][k] for
  * i < m, x bf16 rows of stride ldx elements, y (BF16 or F32) rows of stride ldy
- * elements. fp32 accumulation. m == 1 runs the streaming GEMV; larger m runs
- * the MFMA dequant-GEMM, which first rewrites x into MFMA operand order in
- * `workspace` (device memory, 16-byte aligned, caller-owned; at least
- * spiral_mul_mat_workspace_bytes() bytes, which is 0 when the GEMV runs, in
- * which case workspace may be NULL). A workspace must not be shared by calls
- * in flight at the same time. */
+ * elements. fp32 accumulation. m == 1 runs the streaming GEMV; 2 <= m <= 16
+ * (decode batches, speculative decoding) runs the weight-streaming MFMA form,
+ * which reads every weight byte once; larger m runs the MFMA dequant-GEMM,
+ * which first rewrites x into MFMA operand order in `workspace` (device
+ * memory, 16-byte aligned, caller-owned; at least
+ * spiral_mul_mat_workspace_bytes() bytes, which is 0 for m <= 16, in which
+ * case workspace may be NULL). A workspace must not be shared by calls in
+ * flight at the same time. The small-batch form needs y within 2 GiB
+ * ((m - 1) * ldy + n_rows elements), else SPIRAL_ERR_SHAPE. */
 int64_t spiral_mul_mat_workspace_bytes(int type, int64_t n_rows, int64_t k,
                                        int64_t m);
 int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k,

@@ -8,6 +8,9 @@ int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, 
 int64_t gemm_workspace_bytes(int64_t m, int64_t k);
 int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m,
          void* y, int y_type, int64_t ldy, void* workspace, hipStream_t s);
+bool skinny_fits(int type, int64_t n_rows, int64_t k, int64_t m);
+int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
+           int y_type, int64_t ldy, hipStream_t s);
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs);
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
@@ -21,6 +24,7 @@ extern "C" {
 int64_t spiral_mul_mat_workspace_bytes(int type, int64_t n_rows, int64_t k, int64_t m) {
   if (!is_quant_type(type) || n_rows <= 0 || m <= 0 || k <= 0 || k % block_elems(type) != 0) return 0;
   if (m == 1 && k <= gemv_max_k(type)) return 0;
+  if (skinny_fits(type, n_rows, k, m)) return 0;
   return gemm_workspace_bytes(m, k);
 }
 
@@ -43,7 +47,10 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uin
   int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (need == 0) return gemv(type, w, n_rows, k, x, y, y_type, s);
+  if (need == 0) {
+    if (m == 1) return gemv(type, w, n_rows, k, x, y, y_type, s);
+    return skinny(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
+  }
   return gemm(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, workspace, s);
 }
 

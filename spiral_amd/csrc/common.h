@@ -115,4 +115,9 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Compute units of the current device (cached per device id).
 int device_cu_count();
 
+// Workgroups of `kernel` resident per CU at `threads` threads and `lds` bytes
+// of dynamic LDS (hipOccupancyMaxActiveBlocksPerMultiprocessor, cached; 1 when
+// the query fails).
+int blocks_per_cu(const void* kernel, int threads, int64_t lds);
+
 }  // namespace spiral

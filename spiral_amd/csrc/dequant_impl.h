@@ -106,7 +106,11 @@ __device__ __forceinline__ Planes make_planes(const uint8_t* w, int64_t n_rows, 
   Planes P;
   if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
     P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 16));
-    P.d = buffer_rsrc(w + tot * 16, static_cast<uint32_t>(tot * 2));
+    // d plane rounded up to whole dwords: a dword load of the last d (at a
+    // 4-byte aligned address, so inside the same page) then reads it instead
+    // of failing the range check; the 2 bytes past the plane are only ever
+    // taken for blocks past the row's end, whose d is forced to 0.
+    P.d = buffer_rsrc(w + tot * 16, static_cast<uint32_t>((tot * 2 + 3) & ~int64_t(3)));
     P.b = P.c = P.a;
   } else if constexpr (TYPE == SPIRAL_TYPE_Q8_0) {
     P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 32));
@@ -124,6 +128,9 @@ __device__ __forceinline__ Planes make_planes(const uint8_t* w, int64_t n_rows, 
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
 }
 __device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);

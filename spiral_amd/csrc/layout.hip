@@ -8,6 +8,7 @@
 // (subnormal scales keep their bits; the kernels decode exponent 0 as +0, the
 // value the reference's flush produces).
 #include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #include "common.h"
@@ -38,6 +39,38 @@ int device_cu_count() {
     cache[dev] = cus;
   }
   return cache[dev];
+}
+
+// Resident workgroups per CU of a kernel at an LDS size (occupancy API,
+// cached per device, kernel and LDS size).
+int blocks_per_cu(const void* kernel, int threads, int64_t lds) {
+  struct Key {
+    int dev;
+    const void* kernel;
+    int64_t lds;
+    bool operator==(const Key& o) const { return dev == o.dev && kernel == o.kernel && lds == o.lds; }
+  };
+  struct Hash {
+    size_t operator()(const Key& k) const {
+      return std::hash<const void*>()(k.kernel) ^ (std::hash<int64_t>()(k.lds) * 31u) ^ static_cast<size_t>(k.dev);
+    }
+  };
+  static std::mutex mu;
+  static std::unordered_map<Key, int, Hash> cache;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const Key key{dev, kernel, lds};
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, static_cast<size_t>(lds)) != hipSuccess ||
+      n <= 0) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  cache.emplace(key, n);
+  return n;
 }
 
 namespace {

@@ -274,7 +274,13 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
 
 constexpr int kMoeKC = 768;                   // k chunk of activations staged in LDS (3 pairs)
 constexpr int kMoeTok = 16;                   // tokens per pass (one MFMA row block)
-constexpr int kMoeAPitch = kMoeKC + 8;        // bf16 per staged row
+// Staged activation rows are padded by kAPad bf16 (64 bytes): an MFMA A
+// read has lane (row r, group g) at byte 64 s + 16 g of row r, so a row
+// offset of 64 bytes puts the 16 (r mod 4, g) starts on 16 different groups
+// of 4 banks (a 16-byte pad would put rows r and r + 1 on the banks of
+// groups g and g + 1).
+constexpr int kAPad = 32;
+constexpr int kMoeAPitch = kMoeKC + kAPad;    // bf16 per staged row
 constexpr int kFusedPairs = 1024;             // largest batch routed inside moe_kernel
 constexpr int kStageAhead = 3;                // weight pairs in flight in registers
 static_assert(kMoeKC % 256 == 0, "activation chunks hold whole weight pairs");
@@ -498,7 +504,7 @@ __global__ void __launch_bounds__(256) moe_kernel(const uint8_t* __restrict__ w,
   const int r = 16 * wave + (lane & 15);            // its row within the stage
   const int64_t nb = k / block_elems(TYPE);
   const int64_t steps = (k + 127) / 128, pairs = (steps + 1) / 2;
-  constexpr int kStepsPerChunk = kMoeKC / 128, kPairsPerChunk = kMoeKC / 256;
+  constexpr int kPairsPerChunk = kMoeKC / 256;
   const Planes P = make_planes<TYPE>(w + e * expert_stride, n_rows, nb);
   const typename WStage<TYPE>::Addr wa = WStage<TYPE>::addr(n0, n_rows, nb, tid);
 
@@ -685,8 +691,9 @@ struct Unit {
 template <>
 struct Unit<SPIRAL_TYPE_Q4_0> {
   static constexpr int kSteps = 2;
-  uint4 qa, qb;    // rows lane / 8 and 8 + lane / 8 of the group, block 8 u + lane % 8
-  uint32_t d0, d1;  // row lane / 4: d of blocks 8 u + 2 (lane % 4) and + 1
+  uint4 qa, qb;      // rows lane / 8 and 8 + lane / 8 of the group, block 8 u + lane % 8
+  uint32_t dl, dh;  // row lane / 4: the dwords holding d of blocks 8 u + 2 (lane % 4) and + 1
+  int32_t dinfo;    // 4 (8 u + 2 (lane % 4) - nb) + byte offset of that d in dl
   struct Addr {
     uint32_t qa, qb, d;
     int c, dc;
@@ -700,19 +707,28 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
     a.d = static_cast<uint32_t>((min(row0 + (lane >> 2), n_rows - 1) * nb + a.dc) * 2);
     return a;
   }
-  // Every load is issued (a load under a branch, or a value combined from
-  // loads here, makes the compiler wait for the ring's loads at once).
-  // Blocks past nb read d = 0 through an offset past the buffer's range, so
-  // their pieces are zero whatever their codes (the next row's bytes, or
-  // zero past the plane).
+  // Every load is issued and every value is a whole loaded dword (a load
+  // under a branch, or a narrower load whose widening the compiler places
+  // elsewhere, makes it wait for all of the ring's loads at once). The pair
+  // of fp16 d sits at an even byte offset: the two dwords around it are
+  // loaded and joined in piece(). Blocks past nb get d = 0 there, so their
+  // pieces are zero whatever their codes (the next row's bytes, or zero past
+  // the plane).
   __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t nb) {
     const int64_t b = 8 * u;
     const uint32_t sq = static_cast<uint32_t>(b * 16), sd = static_cast<uint32_t>(b * 2);
-    constexpr uint32_t kOut = 0x80000000u;  // beyond every plane (experts are < 2 GiB)
     qa = bload16(P.a, a.qa, sq);
     qb = bload16(P.a, a.qb, sq);
-    d0 = bload2(P.d, b + a.dc < nb ? a.d + sd : kOut, 0u);
-    d1 = bload2(P.d, b + a.dc + 1 < nb ? a.d + 2 + sd : kOut, 0u);
+    const uint32_t od = a.d + sd;
+    dl = bload4(P.d, od & ~3u, 0u);
+    dh = bload4(P.d, (od & ~3u) + 4u, 0u);
+    dinfo = static_cast<int32_t>(b + a.dc - nb) * 4 + static_cast<int32_t>(od & 3u);
+  }
+  // d of blocks 8 u + 2 (lane % 4) (bits 0..15) and + 1 (bits 16..31).
+  __device__ __forceinline__ uint32_t d_pair() const {
+    const uint32_t pair = __builtin_amdgcn_alignbyte(dh, dl, static_cast<uint32_t>(dinfo & 3));
+    const int32_t past = dinfo >> 2;  // first block - nb
+    return past >= 0 ? 0u : past == -1 ? pair & 0xffffu : pair;
   }
   // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16).
   __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
@@ -727,8 +743,8 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
       q[j] = (r & 8) ? x1 : x0;
     }
     out.q = make_uint4(q[0], q[1], q[2], q[3]);
-    const uint32_t dd = d0 | (d1 << 16);
-    const uint32_t dv = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(((r << 2) + (b >> 1)) << 2, static_cast<int>(dd)));
+    const uint32_t dv =
+        static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(((r << 2) + (b >> 1)) << 2, static_cast<int>(d_pair())));
     out.d = (b & 1) ? dv >> 16 : dv & 0xffffu;
   }
 };
@@ -794,7 +810,7 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   const int g = lane >> 4;
   const int64_t nb = k / block_elems(TYPE);
   const int64_t steps = (k + 127) / 128;
-  const int pitch = static_cast<int>(steps * 128 + 8);
+  const int pitch = static_cast<int>(steps * 128 + kAPad);
   const Planes P = make_planes<TYPE>(w + e * expert_stride, n_rows, nb);
   // This wave's groups: ordinals j = 0 .. my_groups - 1, group wave + 8 j.
   const int64_t groups = (r1 - r0 + 15) / 16;
@@ -906,7 +922,7 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
 // Dynamic LDS of the streaming form for k (0 when it does not fit).
 int64_t stream_lds_bytes(int64_t k) {
   if (k > kStreamMaxK) return 0;
-  return kMoeTok * (((k + 127) / 128) * 128 + 8) * 2;
+  return kMoeTok * (((k + 127) / 128) * 128 + kAPad) * 2;
 }
 
 template <int TYPE, bool F32_OUT>
@@ -935,7 +951,281 @@ int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_
   return launch_status();
 }
 
+// ---- dense small-batch form (ggml MUL_MAT with 2 .. 16 rows of x) --------
+//
+// The streaming form without routing: the m <= kMoeTok rows of x are the
+// MFMA A rows, and every weight byte is read once. A dense matrix has far
+// fewer 16-row groups than the chip has waves (256 for 4096 rows), so the 8
+// waves of a workgroup work on a "block" of 8 / parts groups, `parts` waves
+// per group, each over its own slice of k; the slices' partial sums meet in
+// LDS at the end of the block (in slice order, so results do not depend on
+// timing). Workgroups are persistent: workgroup b takes blocks b, b + grid,
+// ..., stages x once and streams its blocks end to end through each wave's
+// register ring, whose loads run ahead across block ends.
+//
+// Windows: when m rows of x over the whole k do not fit the LDS budget, k is
+// cut into n_win windows of whole units (balanced, each holding at least
+// `parts` units), staged one after the other within every block; every wave
+// owns a slice of every window, so all waves meet the same barriers. Weight
+// loads do not depend on x, so the ring keeps running across window ends.
+constexpr int kSkinnyThreads = 512;
+constexpr int kSkinnyWaves = kSkinnyThreads / 64;
+constexpr int64_t kSkinnyLds = 152 * 1024;               // activation window + partial sums
+constexpr int kSkinnyRed = 2 * kSkinnyWaves * 4 * 64 * 4;  // partial sums, two blocks' worth
+
+struct SkinnyShape {
+  int parts, n_win;
+  int64_t groups, units, win_units, lds;
+};
+
+// WINDOWS: n_win > 1 (restaging inside the loop). Without it the loop body
+// issues no memory instruction under a branch: the output stores are buffer
+// stores that every lane executes (lanes with nothing to store point past the
+// buffer, and the hardware drops them), so the compiler can count the ring's
+// loads in flight and wait for exactly the one it needs.
+template <int TYPE, bool F32_OUT, bool WINDOWS>
+__global__ void __launch_bounds__(kSkinnyThreads) skinny_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
+                                                                int64_t k, const uint16_t* __restrict__ x,
+                                                                int64_t ldx, int m, void* __restrict__ y,
+                                                                int64_t ldy, int parts, int n_win, int pitch) {
+  extern __shared__ __align__(16) uint16_t As[];  // m rows of `pitch` bf16, then the partial sums
+  __shared__ int64_t s_xrow[kMoeTok];
+  using U = Unit<TYPE>;
+  constexpr int R = kStreamRing<TYPE>;
+  constexpr uint32_t kEsize = F32_OUT ? 4 : 2;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int per_block = kSkinnyWaves / parts;
+  const int gslot = wave / parts, part = wave - gslot * parts;
+  const int64_t groups = (n_rows + 15) / 16;
+  const int64_t n_blocks = (groups + per_block - 1) / per_block;
+  // blocks blockIdx.x + gridDim.x i, i < my_blocks (the grid is at most n_blocks)
+  const int my_blocks = static_cast<int>((n_blocks - 1 - blockIdx.x) / gridDim.x + 1);
+  const auto row0_of = [&](int i) {
+    return ((static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(gridDim.x) * i) * per_block + gslot) * 16;
+  };
+  const int64_t nb = k / block_elems(TYPE);
+  const int64_t steps = (k + 127) / 128;
+  const int units = static_cast<int>((steps + U::kSteps - 1) / U::kSteps);
+  const Planes P = make_planes<TYPE>(w, n_rows, nb);
+  // y as a buffer of (m - 1) ldy + n_rows elements (below 2^31 bytes)
+  const __amdgpu_buffer_rsrc_t Y = buffer_rsrc(y, static_cast<uint32_t>(((m - 1) * ldy + n_rows) * kEsize));
+  float* red = reinterpret_cast<float*>(As + m * pitch);  // [2][8 waves][4][64]
+  if (tid < kMoeTok) s_xrow[tid] = static_cast<int64_t>(min(tid, m - 1)) * ldx;
+
+  // Window v holds units [wb(v), wb(v + 1)); this wave owns slice(v, part) .. slice(v, part + 1).
+  const auto wb = [&](int v) {
+    return WINDOWS ? static_cast<int>(static_cast<int64_t>(units) * v / n_win) : v * units;
+  };
+  const auto slice = [&](int v, int p) { return wb(v) + (wb(v + 1) - wb(v)) * p / parts; };
+  int per_blk_units = 0;
+  for (int v = 0; v < (WINDOWS ? n_win : 1); ++v) per_blk_units += slice(v, part + 1) - slice(v, part);
+  const int n_units = my_blocks * per_blk_units;
+
+  // Load pointer: block lb, window lv, unit lu, end of this wave's slice le.
+  U ring[R];
+  typename U::Addr la = U::addr(row0_of(0), n_rows, nb, lane);
+  int lb = 0, lv = 0, lu = slice(0, part), le = slice(0, part + 1), nl = 0;
+  const auto issue = [&](int s) {
+    ring[s].load(P, la, lu, nb);
+    if (++nl < n_units && ++lu == le) {  // past the last unit the ring re-reads it
+      if (!WINDOWS || ++lv == n_win) {
+        lv = 0;
+        la = U::addr(row0_of(++lb), n_rows, nb, lane);
+      }
+      lu = slice(lv, part);
+      le = slice(lv, part + 1);
+    }
+  };
+  const auto stage = [&](int v) {
+    const int64_t c0 = static_cast<int64_t>(wb(v)) * U::kSteps * 128;
+    const int width = (wb(v + 1) - wb(v)) * U::kSteps * 128;
+    moe_stage<TYPE>(As, x, s_xrow, m, k, c0, tid, width, pitch, kSkinnyThreads);
+  };
+  // x first: its loads complete in order ahead of the ring's.
+  __syncthreads();
+  stage(0);
+#pragma unroll
+  for (int i = 0; i < R - 1; ++i) issue(i);
+  __syncthreads();
+
+  // MFMA rows past m read row m - 1; their outputs are dropped.
+  const uint16_t* arow = As + min(lane & 15, m - 1) * pitch + 8 * g;
+  f32x4_t acc[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  int cb = 0, cv = 0, cu = slice(0, part), ce = slice(0, part + 1);  // compute pointer
+  int64_t st0 = 0;                                                   // first k step of window cv
+  const bool ragged = k % 128 != 0;
+  const auto finish_block = [&]() {
+    // acc: lane l holds x rows 4 (l / 16) + i of weight row row0 + l % 16.
+    f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    float* rb = red + (cb & 1) * (kSkinnyWaves * 4 * 64);
+    if (parts > 1) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rb[(wave * 4 + i) * 64 + lane] = sum[i];
+      // every wave is done with this block's partial sums (and with x)
+      __syncthreads();
+      // slices in order (every wave adds them; the first slice's wave stores)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sum[i] = rb[(gslot * parts * 4 + i) * 64 + lane];
+      for (int p = 1; p < parts; ++p) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum[i] += rb[((gslot * parts + p) * 4 + i) * 64 + lane];
+      }
+    } else if (WINDOWS && cb + 1 < my_blocks) {
+      __syncthreads();  // every wave is done with x
+    }
+    // Lanes with nothing to store set bit 31 of the offset (past the buffer);
+    // bit arithmetic, not a select, so no branch forms around the stores.
+    const int64_t n = row0_of(cb) + (lane & 15);
+    const uint32_t skip = static_cast<uint32_t>(part != 0) | static_cast<uint32_t>(n >= n_rows);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 4 * g + i;
+      const uint32_t bad = (skip | static_cast<uint32_t>(t >= m)) << 31;
+      const uint32_t off = (static_cast<uint32_t>(min(t, m - 1) * ldy + min(n, n_rows - 1)) * kEsize) | bad;
+      if constexpr (F32_OUT)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum[i]), Y, off, 0, 0);
+      else
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, static_cast<__bf16>(sum[i])), Y, off, 0,
+                                              0);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (WINDOWS && cb + 1 < my_blocks) {
+      stage(0);
+      __syncthreads();
+    }
+    ++cb;
+  };
+  const auto compute = [&](int slot) {
+#pragma unroll
+    for (int h = 0; h < U::kSteps; ++h) {
+      const int64_t st = static_cast<int64_t>(cu) * U::kSteps + h;
+      if (U::kSteps == 1 || st < steps) {
+        MoePiece<TYPE> pc;
+        ring[slot].piece(pc, h, lane);
+        if constexpr (TYPE != SPIRAL_TYPE_Q4_0 && TYPE != SPIRAL_TYPE_Q6_K) {
+          if (ragged && st == steps - 1 && 32 * (4 * st + g) >= k) pc.zero();
+        }
+        pc.prep();
+        const uint16_t* ak = arow + 8 * 16 * (st - st0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const bf16x8_t b = __builtin_bit_cast(bf16x8_t, pc.dequant(s));
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ak + 8 * 4 * s);
+          acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[s], 0, 0, 0);
+        }
+      }
+    }
+    if (++cu == ce) {
+      if (WINDOWS && cv + 1 < n_win) {
+        // next window: every wave is done with this one before it is replaced
+        ++cv;
+        __syncthreads();
+        stage(cv);
+        __syncthreads();
+      } else {
+        finish_block();
+        cv = 0;
+      }
+      cu = slice(cv, part);
+      ce = slice(cv, part + 1);
+      st0 = static_cast<int64_t>(wb(cv)) * U::kSteps;
+    }
+  };
+  int i0 = 0;
+  for (; i0 + R <= n_units; i0 += R) {
+#pragma unroll
+    for (int d = 0; d < R; ++d) {
+      issue((d + R - 1) % R);
+      compute(d);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < R - 1; ++d) {
+    if (i0 + d < n_units) compute(d);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the ring's last (repeated) loads
+}
+
+// Slices of k per group and windows of k for m rows of x (parts = 0: the
+// shape does not fit this form).
+SkinnyShape skinny_shape(int type, int64_t n_rows, int64_t k, int64_t m) {
+  SkinnyShape sh{};
+  const int64_t ksteps = type == SPIRAL_TYPE_Q4_0 ? 2 : 1;
+  sh.groups = ceil_div(n_rows, 16);
+  sh.units = ceil_div(ceil_div(k, 128), ksteps);
+  // Widest window (in units) whose activations fit next to the partial sums.
+  const int64_t fit = ((kSkinnyLds - kSkinnyRed) / (2 * m) - kAPad) / (128 * ksteps);
+  if (fit < 1) return sh;
+  sh.n_win = static_cast<int>(ceil_div(sh.units, fit));
+  sh.win_units = ceil_div(sh.units, sh.n_win);
+  // As many slices as the windows allow (up to one wave per slice): the
+  // finest blocks, so the persistent grid divides the work evenly.
+  const int64_t min_win = sh.units / sh.n_win;
+  int parts = 1;
+  while (parts < kSkinnyWaves && 2 * parts <= min_win) parts *= 2;
+  sh.parts = parts;
+  sh.lds = 2 * m * (128 * ksteps * sh.win_units + kAPad) + kSkinnyRed;
+  return sh;
+}
+
+template <int TYPE, bool F32_OUT, bool WINDOWS>
+int launch_skinny(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
+                  int64_t ldy, const SkinnyShape& sh, hipStream_t s) {
+  const auto kern = skinny_kernel<TYPE, F32_OUT, WINDOWS>;
+  static bool attr_set = false;  // benign race: every caller sets the same value
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kSkinnyLds)) != hipSuccess) {
+      (void)hipGetLastError();
+      return SPIRAL_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  const int64_t n_blocks = ceil_div(sh.groups, kSkinnyWaves / sh.parts);
+  const int64_t resident =
+      static_cast<int64_t>(device_cu_count()) * blocks_per_cu(reinterpret_cast<const void*>(kern), kSkinnyThreads, sh.lds);
+  const int pitch = static_cast<int>(128 * Unit<TYPE>::kSteps * sh.win_units + kAPad);
+  const dim3 grid(static_cast<unsigned>(std::min(n_blocks, resident)));
+  hipLaunchKernelGGL(kern, grid, dim3(kSkinnyThreads), static_cast<size_t>(sh.lds), s,
+                     static_cast<const uint8_t*>(w), n_rows, k, x, ldx, static_cast<int>(m), y, ldy, sh.parts,
+                     sh.n_win, pitch);
+  return launch_status();
+}
+
 }  // namespace
+
+// Whether the dense small-batch form takes this product.
+bool skinny_fits(int type, int64_t n_rows, int64_t k, int64_t m) {
+  if (m < 2 || m > kMoeTok) return false;
+  // weight planes are addressed with 32-bit offsets, past-the-end reads at 2^31
+  if (spiral_tensor_bytes(type, n_rows, k) >= (int64_t(1) << 31)) return false;
+  return skinny_shape(type, n_rows, k, m).parts > 0;
+}
+
+// Arguments validated by the caller; skinny_fits() holds.
+int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
+           int y_type, int64_t ldy, hipStream_t s) {
+  const SkinnyShape sh = skinny_shape(type, n_rows, k, m);
+  const bool f32 = y_type == SPIRAL_TYPE_F32;
+  // y is written through a buffer resource with 32-bit offsets
+  if (((m - 1) * ldy + n_rows) * (f32 ? 4 : 2) >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
+#define SPIRAL_SKINNY(T)                                                                     \
+  do {                                                                                        \
+    if (sh.n_win > 1)                                                                         \
+      return f32 ? launch_skinny<T, true, true>(w, n_rows, k, x, ldx, m, y, ldy, sh, s)      \
+                 : launch_skinny<T, false, true>(w, n_rows, k, x, ldx, m, y, ldy, sh, s);    \
+    return f32 ? launch_skinny<T, true, false>(w, n_rows, k, x, ldx, m, y, ldy, sh, s)       \
+               : launch_skinny<T, false, false>(w, n_rows, k, x, ldx, m, y, ldy, sh, s);     \
+  } while (0)
+  if (type == SPIRAL_TYPE_Q4_0) SPIRAL_SKINNY(SPIRAL_TYPE_Q4_0);
+  if (type == SPIRAL_TYPE_Q8_0) SPIRAL_SKINNY(SPIRAL_TYPE_Q8_0);
+  SPIRAL_SKINNY(SPIRAL_TYPE_Q6_K);
+#undef SPIRAL_SKINNY
+}
 
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_expert + 1 + n_pairs); }
 

@@ -110,8 +110,13 @@ def test_sizes(spiral_lib):
     assert L.spiral_tensor_bytes(_lib.TYPE_Q6_K, 4096, 14336) == 48_168_960
     assert L.spiral_tensor_bytes(_lib.TYPE_Q4_0, 4096, 4096) == 9_437_184
     assert L.spiral_mul_mat_id_workspace_bytes(128, 64, 8) == 4 * (129 + 512)
-    # GEMV (m = 1) needs no workspace; the GEMM packs m rows (rounded up to 16) of k bf16
+    # GEMV (m = 1) and the small-batch form (m = 2..16) need no workspace; the
+    # GEMM packs m rows (rounded up to 16) of k bf16
     assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q8_0, 14336, 4096, 1) == 0
+    for m in (2, 4, 16):
+        assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q4_0, 14336, 4096, m) == 0
+        assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q6_K, 4096, 14336, m) == 0
+    assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q4_0, 4096, 4096, 17) == 32 * 4096 * 2
     assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q4_0, 4096, 4096, 512) == 512 * 4096 * 2
     assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q4_0, 4096, 4096, 130) == 144 * 4096 * 2
     assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q6_K, 4096, 100, 4) == 0  # k not a block multiple
@@ -132,10 +137,12 @@ def test_validation_before_device_work(spiral_lib):
     assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 1, p, _lib.TYPE_I32, 4, None, 0, None) == 6
     assert L.spiral_mul_mat(q4, p, 4, 64, p, 60, 1, p, _lib.TYPE_F32, 4, None, 0, None) == 1
     assert L.spiral_mul_mat(_lib.TYPE_Q6_K, p, 4, 64, p, 64, 1, p, _lib.TYPE_F32, 4, None, 0, None) == 1
-    # the GEMM path (m > 1) needs its workspace: missing -> NULL, short -> CAPACITY, misaligned -> ALIGN
-    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 8, p, _lib.TYPE_F32, 4, None, 0, None) == 3
-    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 8, p, _lib.TYPE_F32, 4, p, 16 * 64 * 2 - 1, None) == 7
-    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 8, p, _lib.TYPE_F32, 4, ctypes.c_void_p(4104), 4096, None) == 2
+    # the GEMM path (m > 16) needs its workspace: missing -> NULL, short -> CAPACITY, misaligned -> ALIGN
+    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, None, 0, None) == 3
+    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, p, 32 * 64 * 2 - 1, None) == 7
+    assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, ctypes.c_void_p(4104), 8192, None) == 2
+    # the small-batch form (m = 2..16) takes none
+    assert L.spiral_mul_mat(q4, p, 4, 64, p, 60, 8, p, _lib.TYPE_F32, 4, None, 0, None) == 1
     assert L.spiral_get_rows(q4, p, 4, 64, p, 0, p, _lib.TYPE_F32, 64, None) == 0  # empty is a no-op
     assert L.spiral_mul_mat_id(q4, p, 32, 4, 4, 64, p, 3, p, 2, 2, p, _lib.TYPE_F32, p, 1 << 20, None) == 1
     assert L.spiral_mul_mat_id(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, p, _lib.TYPE_F32, p, 4, None) == 7
@@ -143,5 +150,6 @@ def test_validation_before_device_work(spiral_lib):
     if L.spiral_device_count() == 0:
         assert L.spiral_dequant_bf16(q4, p, 4, 64, p, 64, None) == 4
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 1, p, _lib.TYPE_F32, 4, None, 0, None) == 4
-        assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 8, p, _lib.TYPE_F32, 4, p, 4096, None) == 4
+        assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, p, 8192, None) == 4
+        assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 8, p, _lib.TYPE_F32, 4, None, 0, None) == 4
         assert L.quants_unpack_all(q4, p, 64, 8, p, None) == 4

@@ -195,6 +195,57 @@ def test_gemm_ragged(cuda, qtype, m, n, k_blocks):
     assert rel_err(y, ref) <= REL_TOL_EXACT_W, rel_err(y, ref)
 
 
+# ---- small batches (2..16 rows of x: the weight-streaming MFMA form) ------------
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("m", [2, 3, 4, 8, 16])
+def test_mul_mat_small_batch(cuda, qtype, m):
+    # 300 rows (a ragged last 16-row group); Q4_0 / Q8_0 k not a multiple of 128
+    k = O.BLOCK_ELEMS[qtype] * (13 if qtype != O.Q6_K else 5)
+    y, ref = _mul_mat_case(cuda, qtype, 300, k, m, 40 + m, torch.float32)
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W, rel_err(y, ref)
+
+
+@pytest.mark.parametrize("qtype,n,k", [(O.Q4_0, 7, 32), (O.Q8_0, 16, 64), (O.Q6_K, 5, 256)])
+def test_mul_mat_small_batch_tiny(cuda, qtype, n, k):
+    """Fewer rows than one MFMA group and a single block or super-block of k."""
+    for m in (2, 16):
+        y, ref = _mul_mat_case(cuda, qtype, n, k, m, 50 + m, torch.float32)
+        assert rel_err(y, ref) <= REL_TOL_EXACT_W, (m, rel_err(y, ref))
+
+
+@pytest.mark.parametrize("qtype,k", [(O.Q4_0, 8192), (O.Q8_0, 8192), (O.Q6_K, 14336)])
+def test_mul_mat_small_batch_k_windows(cuda, qtype, k):
+    """16 rows of x over this k exceed the LDS window: k is staged in windows."""
+    y, ref = _mul_mat_case(cuda, qtype, 200, k, 16, 60, torch.float32)
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W, rel_err(y, ref)
+
+
+def test_mul_mat_small_batch_strides(cuda):
+    """x rows and y rows with strides wider than k and n."""
+    qtype, n, k, m = O.Q4_0, 100, 256, 5
+    raw = synth.make_weights(qtype, n, k, 70)
+    x = synth.make_x(m, k, 71)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    xw = torch.zeros((m, k + 24), dtype=torch.bfloat16, device=cuda)
+    xw[:, :k] = dev_bf16(x, cuda)
+    yw = torch.full((m, n + 12), 7.0, dtype=torch.float32, device=cuda)
+    ops.mul_mat(qtype, w, n, k, xw[:, :k], out=yw[:, :n])
+    torch.cuda.synchronize()
+    ref = O.matmul_f64(O.dequant(qtype, raw, n, k), x)
+    got = yw.cpu().numpy()
+    assert rel_err(got[:, :n], ref) <= REL_TOL_EXACT_W
+    assert (got[:, n:] == 7.0).all()  # nothing written past n
+
+
+@pytest.mark.parametrize("qtype,n,k", [(O.Q4_0, 14336, 4096), (O.Q8_0, 14336, 4096), (O.Q6_K, 4096, 14336)])
+def test_mul_mat_small_batch_workload_shapes(cuda, qtype, n, k):
+    y, ref = _mul_mat_case(cuda, qtype, n, k, 4, 5, torch.bfloat16)
+    err = rel_err(y, ref)
+    print(f"mul_mat m=4 {NAMES[qtype]} {n}x{k}: rel err {err:.2e}")
+    assert err <= REL_TOL
+
+
 def test_gemm_q4_0_prefill_512x4096x4096(cuda):
     y, ref = _mul_mat_case(cuda, O.Q4_0, 4096, 4096, 512, 4, torch.bfloat16)
     err = rel_err(y, ref)
