@@ -667,10 +667,12 @@ struct PieceAddr<SPIRAL_TYPE_Q6_K> {
 
 // What one ring slot of the streaming form holds (a "unit"), loaded for one
 // 16-row group of the wave. Q4_0: a pair of k steps of all 16 rows, loaded
-// as whole 128-byte lines (lanes 8 r' + c: row r', block c of the pair, in
-// two instructions for rows 0..7 and 8..15) and moved into MFMA position
-// with ds_bpermute; loading the pieces directly would fetch every line as
-// two 64-byte halves, which the L1's miss capacity turns into the limit.
+// as whole 128-byte lines (two instructions, rows 0..7 and 8..15) and moved
+// into MFMA position with ds_bpermute; loading the pieces directly would
+// fetch every line as two 64-byte halves, which the L1's miss capacity turns
+// into the limit. Lanes hold the blocks of step h of the pair in lanes
+// 32 h .. 32 h + 31, so the 32 source lanes of each permute are consecutive
+// and fall in distinct LDS banks.
 // Other types: one k step's pieces, loaded directly.
 template <int TYPE>
 struct Unit {
@@ -691,20 +693,23 @@ struct Unit {
 template <>
 struct Unit<SPIRAL_TYPE_Q4_0> {
   static constexpr int kSteps = 2;
-  uint4 qa, qb;      // rows lane / 8 and 8 + lane / 8 of the group, block 8 u + lane % 8
-  uint32_t dl, dh;  // row lane / 4: the dwords holding d of blocks 8 u + 2 (lane % 4) and + 1
-  int32_t dinfo;    // 4 (8 u + 2 (lane % 4) - nb) + byte offset of that d in dl
+  // Lane l = 32 h + 4 r' + c': qa / qb hold rows r' and 8 + r' of the
+  // group, block 8 u + 4 h + c'. Lane l = 32 h + 2 r + p: dl / dh hold the
+  // dwords around d of blocks 8 u + 4 h + 2 p and + 1 of row r.
+  uint4 qa, qb;
+  uint32_t dl, dh;
+  int32_t dinfo;  // 4 (first of the two blocks - nb) + byte offset of its d in dl
   struct Addr {
     uint32_t qa, qb, d;
-    int c, dc;
+    int dc;
   };
   static __device__ __forceinline__ Addr addr(int64_t row0, int64_t n_rows, int64_t nb, int lane) {
     Addr a;
-    a.c = lane & 7;
-    a.dc = 2 * (lane & 3);
-    a.qa = static_cast<uint32_t>((min(row0 + (lane >> 3), n_rows - 1) * nb + a.c) * 16);
-    a.qb = static_cast<uint32_t>((min(row0 + 8 + (lane >> 3), n_rows - 1) * nb + a.c) * 16);
-    a.d = static_cast<uint32_t>((min(row0 + (lane >> 2), n_rows - 1) * nb + a.dc) * 2);
+    const int h = lane >> 5, c = 4 * h + (lane & 3), rq = (lane & 31) >> 2, rd = (lane & 31) >> 1;
+    a.dc = 4 * h + 2 * (lane & 1);
+    a.qa = static_cast<uint32_t>((min(row0 + rq, n_rows - 1) * nb + c) * 16);
+    a.qb = static_cast<uint32_t>((min(row0 + 8 + rq, n_rows - 1) * nb + c) * 16);
+    a.d = static_cast<uint32_t>((min(row0 + rd, n_rows - 1) * nb + a.dc) * 2);
     return a;
   }
   // Every load is issued and every value is a whole loaded dword (a load
@@ -732,8 +737,8 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
   }
   // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16).
   __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
-    const int r = lane & 15, b = 4 * h + (lane >> 4);
-    const int src = (((r & 7) << 3) + b) << 2;
+    const int r = lane & 15, g = lane >> 4, b = 4 * h + g;
+    const int src = (32 * h + 4 * (r & 7) + g) << 2;
     const uint32_t va[4] = {qa.x, qa.y, qa.z, qa.w}, vb[4] = {qb.x, qb.y, qb.z, qb.w};
     uint32_t q[4];
 #pragma unroll
@@ -744,7 +749,7 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
     }
     out.q = make_uint4(q[0], q[1], q[2], q[3]);
     const uint32_t dv =
-        static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(((r << 2) + (b >> 1)) << 2, static_cast<int>(d_pair())));
+        static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((32 * h + 2 * r + (g >> 1)) << 2, static_cast<int>(d_pair())));
     out.d = (b & 1) ? dv >> 16 : dv & 0xffffu;
   }
 };
