@@ -28,7 +28,7 @@
 //    entry e of its 64 tasks touches 1 KiB of consecutive LDS and e is an
 //    immediate offset. Per-task sums of x follow the entries.
 //  - A row's fp32 partial sums are reduced across the wave after its last
-//    pass and lane 0 stores y.
+//    pass with DPP (six adds, the total in lane 63) and lane 63 stores y.
 //
 // Arithmetic (fp32 accumulation throughout):
 //  - Codes are turned into small floats with an exact offset and the offset
@@ -475,8 +475,8 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restr
         acc += ok ? part : 0.0f;
       }
       if (pc == passes - 1) {
-        const float v = wave_sum(acc);
-        if (lane == 0) store_y<F32_OUT>(y, rc, v);
+        const float v = wave_sum_last(acc);
+        if (lane == 63) store_y<F32_OUT>(y, rc, v);
         acc = 0.0f;
       }
       advance(rc, pc);
