@@ -8,8 +8,9 @@ Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
 x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
 workloads under "workloads": Q4_0 GEMV (14336 x 4096), the Q4_0 small-batch
 product at m = 4 (same matrix), Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
-and Q6_K -> bf16 dequant (4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096) and the Q4_0 MoE
-grouped GEMM (128 experts, 64 tokens, top-8).
+and Q6_K -> bf16 dequant (4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096), the Q4_0 MoE
+grouped GEMM (128 experts, 64 tokens, top-8) and its gate_up stage fused with
+SwiGLU.
 
 Measurement
   - Inputs are synthetic and seeded, converted to the planar layout and
@@ -126,7 +127,8 @@ TRAFFIC_KERNELS = {
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
-    "moe_q4_0": (["moe_stream_kernel<2,"], None),
+    "moe_q4_0": (["moe_stream_kernel<2,false,false>"], None),
+    "moe_gate_up_swiglu_q4_0": (["moe_stream_kernel<2,false,true>"], None),
 }
 
 
@@ -345,7 +347,7 @@ def main():
         del ws, xs
 
     # --- Q4_0 MoE grouped GEMM ----------------------------------------------------
-    if want("moe_q4_0"):
+    if want("moe_q4_0") or want("moe_gate_up_swiglu_q4_0"):
         n_expert, hidden, inter2, inter = 128, 2048, 1536, 768
         n_tokens, top_k = 64, 8
         rng = np.random.default_rng(9)
@@ -384,14 +386,30 @@ def main():
             ops.mul_mat_id(TYPE_Q4_0, gus[c], gu_per, n_expert, inter2, hidden, x1, ids_d, workspace=ws1, out=y1)
             ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, x2, ids_d, workspace=ws2, out=y2)
 
-        wall, ev = timer.run(launch, steps, warmup)
-        wbytes = touched * (gu_per + dn_per)
-        flops = 2.0 * n_tokens * top_k * (inter2 * hidden + hidden * inter)
-        record("moe_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
-               {"workload": "Q4_0 MoE: 128 experts (gate_up 1536x2048, down 2048x768), 64 tokens, top-8; "
-                            "one step = gate_up + down MUL_MAT_ID",
-                "bytes_per_launch": wbytes, "touched_experts": int(touched),
-                "tflops": flops / (ev / steps) / 1e12, "copies": copies})
+        if want("moe_q4_0"):
+            wall, ev = timer.run(launch, steps, warmup)
+            wbytes = touched * (gu_per + dn_per)
+            flops = 2.0 * n_tokens * top_k * (inter2 * hidden + hidden * inter)
+            record("moe_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+                   {"workload": "Q4_0 MoE: 128 experts (gate_up 1536x2048, down 2048x768), 64 tokens, top-8; "
+                                "one step = gate_up + down MUL_MAT_ID",
+                    "bytes_per_launch": wbytes, "touched_experts": int(touched),
+                    "tflops": flops / (ev / steps) / 1e12, "copies": copies})
+
+        # gate_up fused with SwiGLU: [64][8][768] bf16, the down stage's input
+        if want("moe_gate_up_swiglu_q4_0"):
+            h = torch.empty((n_tokens, top_k, inter), dtype=torch.bfloat16, device=dev)
+
+            def launch_glu(i):
+                ops.mul_mat_id_glu(TYPE_Q4_0, gus[i % copies], gu_per, n_expert, inter2, hidden, x1, ids_d,
+                                   ops.GLU_SWIGLU, workspace=ws1, out=h)
+
+            wall, ev = timer.run(launch_glu, steps, warmup)
+            wbytes = touched * gu_per
+            record("moe_gate_up_swiglu_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+                   {"workload": "Q4_0 MoE gate_up (128 experts of 1536x2048, 64 tokens, top-8) fused with SwiGLU "
+                                "into the [64][8][768] bf16 down-stage input; one step = one fused MUL_MAT_ID + GLU",
+                    "bytes_per_launch": wbytes, "touched_experts": int(touched), "copies": copies})
         del gus, dns
 
     if not results:

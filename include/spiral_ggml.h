@@ -2,14 +2,15 @@
  * spiral_ggml.h -- a ggml-backend-shaped C surface over libspiral_quants.so:
  * buffer type / buffer / tensor upload, supports_op and graph_compute for
  * MUL_MAT, GET_ROWS and MUL_MAT_ID with quantized (Q4_0 / Q8_0 / Q6_K) src0,
- * on one HIP device.
+ * and GLU (fused into a preceding MUL_MAT_ID when possible), on one HIP
+ * device.
  *
  * The reference names this surface but does not contain it: its README says
  * the NPU backend "will live in a llama.cpp fork" (README.md:11-14) and its
  * repack header is meant to be compiled into that loader
  * (src/quants/common/repack.h:5-7). ggml itself is not vendored. The types
  * below therefore mirror the public ggml-backend interface field for field
- * (ggml_tensor's type / buffer / ne / nb / op / src / data / name, ggml_cgraph's
+ * (ggml_tensor's type / buffer / ne / nb / op / op_params / flags / src / data / name, ggml_cgraph's
  * n_nodes / nodes, ggml_backend_buffer_i's alloc / free / get_base /
  * init_tensor / set_tensor / get_tensor / memset_tensor / clear,
  * ggml_backend_i's graph_compute / synchronize, ggml_backend_device_i's
@@ -41,6 +42,11 @@ extern "C" {
 #define SPIRAL_MAX_DIMS 4
 #define SPIRAL_MAX_SRC 10
 #define SPIRAL_MAX_NAME 64
+#define SPIRAL_MAX_OP_PARAMS 16 /* int32 words, ggml's 64 bytes */
+
+/* ggml tensor flags this backend reads: an OUTPUT tensor is read after the
+ * graph runs, so it is never fused away. */
+#define SPIRAL_TENSOR_FLAG_OUTPUT 2
 
 /* Operations this backend knows (the subset of ggml_op it takes part in).
  * NONE / VIEW / RESHAPE / PERMUTE / TRANSPOSE are no-ops at compute time, as
@@ -53,7 +59,8 @@ typedef enum spiral_op {
   SPIRAL_OP_VIEW = 4,
   SPIRAL_OP_RESHAPE = 5,
   SPIRAL_OP_PERMUTE = 6,
-  SPIRAL_OP_TRANSPOSE = 7
+  SPIRAL_OP_TRANSPOSE = 7,
+  SPIRAL_OP_GLU = 8 /* op_params[0]: SPIRAL_GLU_* variant, op_params[1]: swapped */
 } spiral_op;
 
 typedef struct spiral_buffer spiral_buffer;   /* device memory block (opaque) */
@@ -61,13 +68,16 @@ typedef struct spiral_backend spiral_backend; /* one device + stream (opaque) */
 
 /* ggml_tensor's fields that a backend reads: type (SPIRAL_TYPE_*, the ggml
  * type ids), ne (elements per dimension, ne[0] innermost), nb (byte strides),
- * op and src (the node's inputs), data (device address inside `buffer`). */
+ * op, op_params and flags, src (the node's inputs), data (device address
+ * inside `buffer`). */
 typedef struct spiral_tensor {
   int32_t type;
   spiral_buffer* buffer;
   int64_t ne[SPIRAL_MAX_DIMS];
   size_t nb[SPIRAL_MAX_DIMS];
   int32_t op;
+  int32_t op_params[SPIRAL_MAX_OP_PARAMS];
+  int32_t flags;
   struct spiral_tensor* src[SPIRAL_MAX_SRC];
   void* data;
   char name[SPIRAL_MAX_NAME];
@@ -127,6 +137,10 @@ int spiral_buffer_clear(spiral_buffer* buf, uint8_t value);
  *   MUL_MAT_ID  src0 quantized [k, n, n_expert], src1 F32/BF16
  *               [k, x_slots (1 or top_k), n_tokens], src2 I32 [top_k,
  *               n_tokens], dst F32 [n, top_k, n_tokens], all contiguous;
+ *   GLU         src0 F32 [2F, ...] with contiguous rows and no src1 (the
+ *               single-tensor form), dst F32 [F, ...] of the same outer
+ *               shape; op_params[0] REGLU / GEGLU / SWIGLU / GEGLU_ERF /
+ *               GEGLU_QUICK, op_params[1] 0 or 1;
  *   NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE.
  * Row lengths must be multiples of the type's block (32, Q6_K 256). */
 int spiral_supports_op(const spiral_tensor* op);
@@ -144,7 +158,10 @@ void* spiral_backend_stream(const spiral_backend* be);
  * graph_compute). Fails with SPIRAL_ERR_TYPE, before launching anything, if
  * a node is not supported; device scratch (bf16 copies of F32 activations,
  * MUL_MAT_ID routing lists) is owned by the backend and grows on demand.
- * Asynchronous: returns when the work is queued. */
+ * A MUL_MAT_ID node followed by a GLU node over it runs as one fused pass
+ * (spiral_mul_mat_id_glu) when no other node reads the MUL_MAT_ID result,
+ * it is not flagged OUTPUT and k <= 4096; its own data is then not written,
+ * as with ggml's fusion. Asynchronous: returns when the work is queued. */
 int spiral_backend_graph_compute(spiral_backend* be, const spiral_cgraph* graph);
 /* Waits for the backend's stream (ggml synchronize). */
 int spiral_backend_synchronize(spiral_backend* be);

@@ -184,6 +184,43 @@ int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride,
                       int64_t n_tokens, int64_t top_k, void* y, int y_type,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ggml GLU variants, numbered as ggml's ggml_glu_op: out = act(a) * b over
+ * the two halves (a, b) of a row of 2F values, a the first half unless
+ * swapped. act: REGLU relu, GEGLU gelu (tanh form), SWIGLU silu, GEGLU_ERF
+ * gelu (erf form), GEGLU_QUICK x * sigmoid(1.702 x). SWIGLU_OAI (clamped,
+ * with float parameters) is not implemented. */
+enum {
+  SPIRAL_GLU_REGLU = 0,
+  SPIRAL_GLU_GEGLU = 1,
+  SPIRAL_GLU_SWIGLU = 2,
+  SPIRAL_GLU_SWIGLU_OAI = 3,
+  SPIRAL_GLU_GEGLU_ERF = 4,
+  SPIRAL_GLU_GEGLU_QUICK = 5
+};
+
+/* spiral_mul_mat_id followed by GLU over each output row, in one pass: the
+ * expert matrices have n_rows = 2F rows (gate rows [0, F), up rows [F, 2F),
+ * ggml's merged gate/up layout) and y[t][s][f] = act(g) * u with
+ * g = (W x)[f], u = (W x)[F + f] (act(u) * g when swapped). y is
+ * [n_tokens][top_k][F] of y_type; the [.. ][2F] product is never written.
+ * Other arguments as spiral_mul_mat_id. Implemented for the decode shapes
+ * (k <= 4096; else SPIRAL_ERR_SHAPE); SPIRAL_ERR_TYPE for an unknown or
+ * unimplemented glu_op. No counterpart in the reference, whose MoE path is
+ * a plan (src/quants/TODO.md:55,214-220). */
+int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride,
+                          int64_t n_expert, int64_t n_rows, int64_t k,
+                          const uint16_t* x, int64_t x_slots,
+                          const int32_t* ids, int64_t n_tokens, int64_t top_k,
+                          int glu_op, int swapped, void* y, int y_type,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/* ggml GLU on its own: y[r][f] = act(x[r][f]) * x[r][F + f] (halves swapped
+ * when swapped) for r < rows, f < F; x rows of 2F floats with stride ldx
+ * elements, y rows of stride ldy; F32 in and out, device pointers. */
+int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx,
+               int64_t F, int64_t rows, float* y, int64_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -196,6 +196,42 @@ def matmul_f64_exact(w_f64, x_bf16):
     return y
 
 
+# ggml GLU variants (ggml_glu_op numbering), used by the fused MUL_MAT_ID + GLU.
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = 0, 1, 2, 4, 5
+
+
+def glu_f64(h, op, swapped=False):
+    """ggml's GLU over the last axis of h (..., 2F) in float64: act(a) * b with
+    (a, b) the first and second halves of each row, (b, a) when swapped.
+
+    ggml is not vendored by the reference (its MoE FFN is a plan:
+    src/quants/TODO.md:55,214-220); act follows the published definitions of
+    ggml's GLU ops: REGLU relu; GEGLU gelu in its tanh form
+    0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); SWIGLU silu x / (1 + e^-x);
+    GEGLU_ERF 0.5 x (1 + erf(x / sqrt(2))); GEGLU_QUICK x / (1 + e^(-1.702 x)).
+    """
+    from scipy.special import erf
+
+    h = np.asarray(h, dtype=np.float64)
+    F = h.shape[-1] // 2
+    a, b = h[..., :F], h[..., F:]
+    if swapped:
+        a, b = b, a
+    if op == GLU_REGLU:
+        act = np.maximum(a, 0.0)
+    elif op == GLU_GEGLU:
+        act = 0.5 * a * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (a + 0.044715 * a ** 3)))
+    elif op == GLU_SWIGLU:
+        act = a / (1.0 + np.exp(-a))
+    elif op == GLU_GEGLU_ERF:
+        act = 0.5 * a * (1.0 + erf(a / np.sqrt(2.0)))
+    elif op == GLU_GEGLU_QUICK:
+        act = a / (1.0 + np.exp(-1.702 * a))
+    else:
+        raise ValueError(f"GLU op {op}")
+    return act * b
+
+
 def matmul_f32(w_bf16, x_bf16):
     w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
     x = np.ascontiguousarray(x_bf16, dtype=np.uint16)

@@ -14,7 +14,34 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs);
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, void* workspace, hipStream_t s);
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s);
+int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
+        hipStream_t s);
+
+bool glu_op_ok(int op) {
+  return op == SPIRAL_GLU_REGLU || op == SPIRAL_GLU_GEGLU || op == SPIRAL_GLU_SWIGLU ||
+         op == SPIRAL_GLU_GEGLU_ERF || op == SPIRAL_GLU_GEGLU_QUICK;
+}
+
+// Checks shared by MUL_MAT_ID and its fused GLU form.
+int check_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
+                     const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k,
+                     void* y, int y_type, void* workspace, int64_t workspace_bytes) {
+  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
+  if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
+  if (w == nullptr || x == nullptr || ids == nullptr || y == nullptr || workspace == nullptr)
+    return SPIRAL_ERR_NULL;
+  if (n_expert <= 0 || n_rows <= 0 || k <= 0 || k % block_elems(type) != 0 || n_tokens < 0 || top_k <= 0)
+    return SPIRAL_ERR_SHAPE;
+  if (x_slots != 1 && x_slots != top_k) return SPIRAL_ERR_SHAPE;
+  if (expert_stride < spiral_tensor_bytes(type, n_rows, k) || expert_stride % 16 != 0) return SPIRAL_ERR_SHAPE;
+  if (n_tokens * top_k > INT32_MAX) return SPIRAL_ERR_SHAPE;
+  if (workspace_bytes < moe_workspace_bytes(n_expert, n_tokens * top_k)) return SPIRAL_ERR_CAPACITY;
+  if (!aligned16(w) || !aligned16(x) || k % 8 != 0) return SPIRAL_ERR_ALIGN;
+  if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0 || (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
+    return SPIRAL_ERR_ALIGN;
+  return SPIRAL_OK;
+}
 }  // namespace spiral
 
 using namespace spiral;
@@ -63,24 +90,45 @@ int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_
                       int64_t k, const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens,
                       int64_t top_k, void* y, int y_type, void* workspace, int64_t workspace_bytes,
                       void* stream) {
-  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
-  if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
-  if (n_tokens == 0) return SPIRAL_OK;
-  if (w == nullptr || x == nullptr || ids == nullptr || y == nullptr || workspace == nullptr)
-    return SPIRAL_ERR_NULL;
-  if (n_expert <= 0 || n_rows <= 0 || k <= 0 || k % block_elems(type) != 0 || n_tokens < 0 || top_k <= 0)
-    return SPIRAL_ERR_SHAPE;
-  if (x_slots != 1 && x_slots != top_k) return SPIRAL_ERR_SHAPE;
-  if (expert_stride < spiral_tensor_bytes(type, n_rows, k) || expert_stride % 16 != 0) return SPIRAL_ERR_SHAPE;
-  if (n_tokens * top_k > INT32_MAX) return SPIRAL_ERR_SHAPE;
-  if (workspace_bytes < moe_workspace_bytes(n_expert, n_tokens * top_k)) return SPIRAL_ERR_CAPACITY;
-  if (!aligned16(w) || !aligned16(x) || k % 8 != 0) return SPIRAL_ERR_ALIGN;
-  if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0 || (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
-    return SPIRAL_ERR_ALIGN;
-  int rc = require_device();
+  if (n_tokens == 0 && is_quant_type(type) && (y_type == SPIRAL_TYPE_BF16 || y_type == SPIRAL_TYPE_F32))
+    return SPIRAL_OK;
+  int rc = check_mul_mat_id(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type,
+                            workspace, workspace_bytes);
   if (rc != SPIRAL_OK) return rc;
-  return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type,
+  rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, -1, 0,
              workspace, static_cast<hipStream_t>(stream));
+}
+
+int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,
+                          int64_t k, const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens,
+                          int64_t top_k, int glu_op, int swapped, void* y, int y_type, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
+  if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
+  if (n_tokens == 0 && is_quant_type(type) && (y_type == SPIRAL_TYPE_BF16 || y_type == SPIRAL_TYPE_F32))
+    return SPIRAL_OK;
+  int rc = check_mul_mat_id(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type,
+                            workspace, workspace_bytes);
+  if (rc != SPIRAL_OK) return rc;
+  if (n_rows % 2 != 0) return SPIRAL_ERR_SHAPE;
+  rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, glu_op,
+             swapped, workspace, static_cast<hipStream_t>(stream));
+}
+
+int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx, int64_t F, int64_t rows, float* y, int64_t ldy,
+               void* stream) {
+  if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
+  if (F < 0 || rows < 0 || ldx < 2 * F || ldy < F) return SPIRAL_ERR_SHAPE;
+  if (F == 0 || rows == 0) return SPIRAL_OK;
+  if (x == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
+  if ((reinterpret_cast<uintptr_t>(x) & 3u) != 0 || (reinterpret_cast<uintptr_t>(y) & 3u) != 0)
+    return SPIRAL_ERR_ALIGN;
+  const int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return glu(glu_op, swapped, x, ldx, F, rows, y, ldy, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

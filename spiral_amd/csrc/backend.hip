@@ -1,7 +1,8 @@
 // ggml-backend-shaped surface (include/spiral_ggml.h): buffers that keep
 // quantized tensors in the planar device layout behind a canonical-bytes
 // set/get interface, supports_op, and graph_compute for MUL_MAT / GET_ROWS /
-// MUL_MAT_ID with quantized src0.
+// MUL_MAT_ID with quantized src0, and GLU (fused into the MUL_MAT_ID it
+// follows when nothing else reads that product).
 //
 // The reference only names this layer (README.md:11-14; the repack headers
 // are meant to be compiled into a llama.cpp loader, src/quants/common/
@@ -288,6 +289,50 @@ int compute_mul_mat_id(spiral_backend* be, const spiral_tensor* t) {
                            SPIRAL_TYPE_F32, be->scratch + xbytes, wsb, be->stream);
 }
 
+// MUL_MAT_ID node t with the GLU node g over it as one pass: g's data
+// receives act(gate) * up directly.
+int compute_mul_mat_id_glu(spiral_backend* be, const spiral_tensor* t, const spiral_tensor* g) {
+  const spiral_tensor* a = t->src[0];
+  const spiral_tensor* b = t->src[1];
+  const spiral_tensor* ids = t->src[2];
+  int rc;
+  int64_t ld1, ld2, ld3;
+  const uint16_t* x = act_bf16(b, be->scratch, true, be->stream, ld1, ld2, ld3, rc);
+  if (rc != SPIRAL_OK) return rc;
+  const size_t xbytes = align_up(static_cast<size_t>(b->ne[0] * b->ne[1] * b->ne[2]) * 2, kAlign);
+  const int64_t wsb = spiral_mul_mat_id_workspace_bytes(a->ne[2], ids->ne[1], ids->ne[0]);
+  return spiral_mul_mat_id_glu(a->type, a->data, static_cast<int64_t>(a->nb[2]), a->ne[2], a->ne[1], a->ne[0], x,
+                               b->ne[1], static_cast<const int32_t*>(ids->data), ids->ne[1], ids->ne[0],
+                               g->op_params[0], g->op_params[1], g->data, SPIRAL_TYPE_F32, be->scratch + xbytes, wsb,
+                               be->stream);
+}
+
+// GLU over rows of src0 (contiguous outer dimensions, checked by supports_op).
+int compute_glu(spiral_backend* be, const spiral_tensor* t) {
+  const spiral_tensor* a = t->src[0];
+  const int64_t rows = t->ne[1] * t->ne[2] * t->ne[3];
+  return spiral_glu(t->op_params[0], t->op_params[1], static_cast<const float*>(a->data),
+                    static_cast<int64_t>(a->nb[1] / 4), t->ne[0], rows, static_cast<float*>(t->data),
+                    static_cast<int64_t>(t->nb[1] / 4), be->stream);
+}
+
+// Node i (MUL_MAT_ID) can run fused with node i + 1 (GLU over it): nothing
+// else in the graph reads node i, it is not a graph output, and the fused
+// pass covers its shape.
+bool fusable_glu(const spiral_cgraph* graph, int32_t i) {
+  if (i + 1 >= graph->n_nodes) return false;
+  const spiral_tensor* t = graph->nodes[i];
+  const spiral_tensor* g = graph->nodes[i + 1];
+  if (t->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU || g->src[0] != t) return false;
+  if ((t->flags & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || t->src[0]->ne[0] > 4096) return false;
+  for (int32_t j = 0; j < graph->n_nodes; ++j) {
+    if (j == i + 1) continue;
+    for (int s = 0; s < SPIRAL_MAX_SRC; ++s)
+      if (graph->nodes[j]->src[s] == t) return false;
+  }
+  return true;
+}
+
 int grow_scratch(spiral_backend* be, size_t need) {
   if (need <= be->scratch_size) return SPIRAL_OK;
   int rc = hip_rc(hipStreamSynchronize(be->stream));
@@ -511,6 +556,25 @@ int spiral_supports_op(const spiral_tensor* t) {
       if (n_tokens * top_k > INT32_MAX) return 0;
       return 1;
     }
+    case SPIRAL_OP_GLU: {
+      const spiral_tensor* a = t->src[0];
+      if (a == nullptr || t->src[1] != nullptr) return 0;
+      const int32_t op = t->op_params[0], swapped = t->op_params[1];
+      if (op != SPIRAL_GLU_REGLU && op != SPIRAL_GLU_GEGLU && op != SPIRAL_GLU_SWIGLU && op != SPIRAL_GLU_GEGLU_ERF &&
+          op != SPIRAL_GLU_GEGLU_QUICK)
+        return 0;
+      if (swapped != 0 && swapped != 1) return 0;
+      if (a->type != SPIRAL_TYPE_F32 || t->type != SPIRAL_TYPE_F32) return 0;
+      if (!rows_contiguous(a, 4) || !rows_contiguous(t, 4)) return 0;
+      // Rows evenly strided across the outer dimensions (one row stride).
+      for (const spiral_tensor* u : {a, t})
+        if (u->nb[2] != u->ne[1] * u->nb[1] || u->nb[3] != u->ne[2] * u->nb[2]) return 0;
+      if (a->ne[0] != 2 * t->ne[0]) return 0;
+      for (int d = 1; d < SPIRAL_MAX_DIMS; ++d)
+        if (a->ne[d] != t->ne[d]) return 0;
+      if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0 || (reinterpret_cast<uintptr_t>(t->data) & 3) != 0) return 0;
+      return 1;
+    }
     default:
       return 0;
   }
@@ -557,10 +621,16 @@ int spiral_backend_graph_compute(spiral_backend* be, const spiral_cgraph* graph)
   if (rc != SPIRAL_OK) return rc;
   for (int32_t i = 0; i < graph->n_nodes && rc == SPIRAL_OK; ++i) {
     const spiral_tensor* t = graph->nodes[i];
+    if (fusable_glu(graph, i)) {
+      rc = compute_mul_mat_id_glu(be, t, graph->nodes[i + 1]);
+      ++i;
+      continue;
+    }
     switch (t->op) {
       case SPIRAL_OP_MUL_MAT: rc = compute_mul_mat(be, t); break;
       case SPIRAL_OP_GET_ROWS: rc = compute_get_rows(be, t); break;
       case SPIRAL_OP_MUL_MAT_ID: rc = compute_mul_mat_id(be, t); break;
+      case SPIRAL_OP_GLU: rc = compute_glu(be, t); break;
       default: break;  // views and no-ops
     }
   }

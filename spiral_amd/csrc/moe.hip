@@ -38,6 +38,14 @@
 //    outputs are dropped).
 // Products use exactly dequantized bf16 weights and fp32 accumulation, as in
 // the dense GEMM.
+//
+// GLU fused into the streaming form (ggml MUL_MAT_ID followed by GLU over
+// its two halves, the merged gate/up FFN of MoE models): the expert matrix
+// has 2F rows, gate rows [0, F) and up rows [F, 2F). Workgroups split the F
+// output features; a wave streams feature group j's gate rows and then its
+// up rows through the same register ring, keeps the gate sums, and writes
+// act(gate) * up (act(up) * gate when swapped) to a [pair][F] output, so
+// the [pair][2F] product never reaches memory.
 #include <algorithm>
 
 #include "common.h"
@@ -64,7 +72,7 @@ constexpr int kMoeBN = 64;  // weight rows per workgroup (16 per wave)
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __restrict__ ids, int32_t n_pairs,
                                                               int32_t n_expert, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ list, void* __restrict__ y,
-                                                              int64_t n_rows, int y_f32) {
+                                                              int64_t out_cols, int y_f32) {
   __shared__ int32_t s_cnt[kRouteChunk];
   __shared__ int32_t s_wave[kRouteThreads / 64];
   __shared__ int32_t s_bad[kRouteThreads];
@@ -133,11 +141,11 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
     const int32_t nbad = s_nbad;
     for (int32_t b = 0; b < nbad; ++b) {
       const int64_t row = s_bad[b];
-      for (int64_t col = tid; col < n_rows; col += kRouteThreads) {
+      for (int64_t col = tid; col < out_cols; col += kRouteThreads) {
         if (y_f32)
-          static_cast<float*>(y)[row * n_rows + col] = 0.0f;
+          static_cast<float*>(y)[row * out_cols + col] = 0.0f;
         else
-          static_cast<uint16_t*>(y)[row * n_rows + col] = 0;
+          static_cast<uint16_t*>(y)[row * out_cols + col] = 0;
       }
     }
     __syncthreads();
@@ -591,6 +599,37 @@ __global__ void __launch_bounds__(256) moe_kernel(const uint8_t* __restrict__ w,
 }
 
 
+// ---- GLU activations (ggml GLU ops, fp32) -----------------------------------
+// act(a) * b for the ggml GLU variants (ids as in include/spiral_ggml.h):
+// REGLU relu, GEGLU gelu (tanh form), SWIGLU silu, GEGLU_ERF gelu (erf form),
+// GEGLU_QUICK x * sigmoid(1.702 x).
+__device__ __forceinline__ float glu_act(int op, float a) {
+  switch (op) {
+    case SPIRAL_GLU_REGLU: return a > 0.0f ? a : 0.0f;
+    case SPIRAL_GLU_GEGLU: {
+      const float u = 0.7978845608028654f * a * (1.0f + 0.044715f * a * a);  // sqrt(2/pi) (a + 0.044715 a^3)
+      return 0.5f * a * (1.0f + tanhf(u));
+    }
+    case SPIRAL_GLU_SWIGLU: return a / (1.0f + expf(-a));
+    case SPIRAL_GLU_GEGLU_ERF: return 0.5f * a * (1.0f + erff(a * 0.7071067811865476f));
+    default: return a / (1.0f + expf(-1.702f * a));  // SPIRAL_GLU_GEGLU_QUICK
+  }
+}
+
+// Standalone ggml GLU over rows of 2n floats: y[r][i] = act(h0[i]) * h1[i]
+// with (h0, h1) = (x[r][0 .. n), x[r][n .. 2n)), swapped: the other order.
+__global__ void __launch_bounds__(256) glu_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ y,
+                                                  int64_t ldy, int64_t n, int64_t rows, int op, int swapped) {
+  const int64_t total = n * rows;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = i / n, c = i - r * n;
+    const float* xr = x + r * ldx;
+    const float a = xr[swapped ? c + n : c], b = xr[swapped ? c : c + n];
+    y[r * ldy + c] = glu_act(op, a) * b;
+  }
+}
+
 // ---- streaming form (the decode path) ------------------------------------
 //
 // When the activations of 16 tokens over the whole k fit in LDS (k <= 4096)
@@ -789,12 +828,14 @@ __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32
   }
 }
 
-template <int TYPE, bool F32_OUT>
+// GLU: the fused form above (glu_op, swapped); the output then has n_rows / 2
+// columns and the workgroups' row ranges are over those features.
+template <int TYPE, bool F32_OUT, bool GLU>
 __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     const uint8_t* __restrict__ w, int64_t expert_stride, int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
     int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
-    int64_t rows_per_wg) {
+    int64_t rows_per_wg, int glu_op, int swapped) {
   extern __shared__ __align__(16) uint16_t As[];  // kMoeTok rows of `pitch` bf16
   __shared__ int32_t s_pair[kMoeTok];
   __shared__ int64_t s_xrow[kMoeTok];
@@ -803,11 +844,12 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   constexpr int R = kStreamRing<TYPE>;
   const int64_t e = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t feat = GLU ? n_rows / 2 : n_rows;  // output columns
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
-  const int64_t r1 = min(r0 + rows_per_wg, n_rows);
+  const int64_t r1 = min(r0 + rows_per_wg, feat);
   int32_t begin, end;
   const int32_t* lst;
-  moe_route<F32_OUT>(ids, n_pairs, n_expert, e, offsets, list, s_list, s_n, y, n_rows, r0, r1, tid, kStreamThreads,
+  moe_route<F32_OUT>(ids, n_pairs, n_expert, e, offsets, list, s_list, s_n, y, feat, r0, r1, tid, kStreamThreads,
                      begin, end, lst);
   if (begin >= end || r0 >= r1) return;
 
@@ -821,6 +863,7 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   const int64_t groups = (r1 - r0 + 15) / 16;
   const int64_t my_groups = groups > wave ? (groups - wave + 7) / 8 : 0;
   const int64_t units = (steps + Unit<TYPE>::kSteps - 1) / Unit<TYPE>::kSteps;
+  const int64_t gunits = GLU ? 2 * units : units;  // units per group: gate, then up
   const bool ragged = k % 128 != 0;
   const auto row_of = [&](int64_t j) { return r0 + 16 * (wave + 8 * j) + (lane & 15); };
 
@@ -842,15 +885,19 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     // wait for all of them); past the wave's last unit the ring re-reads it.
     using U = Unit<TYPE>;
     U ring[R];
-    const int n_units = static_cast<int>(my_groups * units);
+    const int n_units = static_cast<int>(my_groups * gunits);
     int lj = 0, lu = 0, nl = 0;
     typename U::Addr la = U::addr(row_of(0) - (lane & 15), n_rows, nb, lane);
     const auto issue = [&](int slot) {
-      ring[slot].load(P, la, lu, nb);
-      if (++nl < n_units && ++lu == units) {
-        lu = 0;
-        ++lj;
-        la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
+      ring[slot].load(P, la, lu < units ? lu : lu - static_cast<int>(units), nb);
+      if (++nl < n_units) {
+        ++lu;
+        if (GLU && lu == units) la = U::addr(feat + row_of(lj) - (lane & 15), n_rows, nb, lane);  // up rows
+        if (lu == gunits) {
+          lu = 0;
+          ++lj;
+          la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
+        }
       }
     };
 #pragma unroll
@@ -864,11 +911,13 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     f32x4_t acc[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4_t gate = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};  // GLU: the group's gate sums
     int cj = 0, cu = 0;  // compute pointer
     const auto compute = [&](int slot) {
+      const int ku = cu < units ? cu : cu - static_cast<int>(units);  // unit within the row
 #pragma unroll
       for (int h = 0; h < U::kSteps; ++h) {
-        const int64_t st = static_cast<int64_t>(cu) * U::kSteps + h;
+        const int64_t st = static_cast<int64_t>(ku) * U::kSteps + h;
         if (U::kSteps == 1 || st < steps) {
           MoePiece<TYPE> pc;
           ring[slot].piece(pc, h, lane);
@@ -886,18 +935,28 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
           }
         }
       }
-      if (++cu == units) {
+      ++cu;
+      if (GLU && cu == units) {
+        gate = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      } else if (cu == gunits) {
         // acc: lane l holds rows 4 (l / 16) + i (routed pairs) of column l % 16.
         const int64_t n = row_of(cj);
-        const f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        if constexpr (GLU) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            sum[i] = swapped ? glu_act(glu_op, sum[i]) * gate[i] : glu_act(glu_op, gate[i]) * sum[i];
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int32_t pr = s_pair[4 * g + i];
           if (pr >= 0 && n < r1) {
             if constexpr (F32_OUT)
-              static_cast<float*>(y)[pr * n_rows + n] = sum[i];
+              static_cast<float*>(y)[pr * feat + n] = sum[i];
             else
-              static_cast<__bf16*>(y)[pr * n_rows + n] = static_cast<__bf16>(sum[i]);
+              static_cast<__bf16*>(y)[pr * feat + n] = static_cast<__bf16>(sum[i]);
           }
         }
 #pragma unroll
@@ -930,11 +989,11 @@ int64_t stream_lds_bytes(int64_t k) {
   return kMoeTok * (((k + 127) / 128) * 128 + kAPad) * 2;
 }
 
-template <int TYPE, bool F32_OUT>
+template <int TYPE, bool F32_OUT, bool GLU>
 int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
                   const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
-                  const int32_t* offsets, const int32_t* list, void* y, hipStream_t s) {
-  const auto kern = moe_stream_kernel<TYPE, F32_OUT>;
+                  const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, hipStream_t s) {
+  const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU>;
   const int64_t lds = stream_lds_bytes(k);
   static bool attr_set = false;  // benign race: every caller sets the same value
   if (!attr_set) {
@@ -946,13 +1005,14 @@ int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_
     attr_set = true;
   }
   // About two workgroups per CU in all, each over a contiguous range of
-  // whole 16-row groups of one expert.
+  // whole 16-row groups of one expert (GLU: of its output features).
+  const int64_t feat = GLU ? n_rows / 2 : n_rows;
   const int64_t per_expert = std::max<int64_t>(1, ceil_div(2 * device_cu_count(), n_expert));
-  const int64_t rows_per_wg = ceil_div(ceil_div(n_rows, per_expert), 16) * 16;
-  const dim3 grid(static_cast<unsigned>(ceil_div(n_rows, rows_per_wg)), static_cast<unsigned>(n_expert));
+  const int64_t rows_per_wg = ceil_div(ceil_div(feat, per_expert), 16) * 16;
+  const dim3 grid(static_cast<unsigned>(ceil_div(feat, rows_per_wg)), static_cast<unsigned>(n_expert));
   hipLaunchKernelGGL(kern, grid, dim3(kStreamThreads), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
                      expert_stride, n_rows, k, x, x_slots, top_k, ids, static_cast<int32_t>(n_pairs),
-                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg);
+                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg, glu_op, swapped);
   return launch_status();
 }
 
@@ -1234,33 +1294,41 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
 
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_expert + 1 + n_pairs); }
 
-// Arguments validated by the caller.
+// Arguments validated by the caller. glu_op < 0: plain MUL_MAT_ID; otherwise
+// the fused GLU form (n_rows even), which only the streaming form implements
+// (k <= kStreamMaxK, else SPIRAL_ERR_SHAPE).
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, void* workspace, hipStream_t s) {
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s) {
   const int64_t n_pairs = n_tokens * top_k;
   const int f32 = y_type == SPIRAL_TYPE_F32;
+  const bool glu = glu_op >= 0;
   // Weight planes of one expert are addressed with 32-bit offsets.
   if (spiral_tensor_bytes(type, n_rows, k) >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
+  if (glu && stream_lds_bytes(k) == 0) return SPIRAL_ERR_SHAPE;
   int32_t* offsets = nullptr;
   int32_t* list = nullptr;
   if (n_pairs > kFusedPairs) {
     offsets = static_cast<int32_t*>(workspace);
     list = offsets + n_expert + 1;
     hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
-                       static_cast<int32_t>(n_expert), offsets, list, y, n_rows, f32);
+                       static_cast<int32_t>(n_expert), offsets, list, y, glu ? n_rows / 2 : n_rows, f32);
     if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
   }
   if (stream_lds_bytes(k) > 0) {
+#define SPIRAL_MOE_STREAM_AS(T, F, G) \
+  launch_stream<T, F, G>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, offsets, list, y, \
+                         glu_op, swapped, s)
 #define SPIRAL_MOE_STREAM(T)                                                                                 \
-  return f32 ? launch_stream<T, true>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, \
-                                      offsets, list, y, s)                                                    \
-             : launch_stream<T, false>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, \
-                                       offsets, list, y, s)
+  do {                                                                                                       \
+    if (glu) return f32 ? SPIRAL_MOE_STREAM_AS(T, true, true) : SPIRAL_MOE_STREAM_AS(T, false, true);        \
+    return f32 ? SPIRAL_MOE_STREAM_AS(T, true, false) : SPIRAL_MOE_STREAM_AS(T, false, false);               \
+  } while (0)
     if (type == SPIRAL_TYPE_Q4_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q4_0);
     if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q8_0);
     SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_MOE_STREAM
+#undef SPIRAL_MOE_STREAM_AS
   }
   const dim3 grid(static_cast<unsigned>(ceil_div(n_rows, kMoeBN)), static_cast<unsigned>(n_expert));
   const uint8_t* W = static_cast<const uint8_t*>(w);
@@ -1279,6 +1347,18 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE(SPIRAL_TYPE_Q8_0);
   else SPIRAL_MOE(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_MOE
+  return launch_status();
+}
+
+// Standalone GLU over `rows` rows of 2n floats; arguments validated by the
+// caller.
+int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
+        hipStream_t s) {
+  const int64_t total = n * rows;
+  if (total == 0) return SPIRAL_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 8 * static_cast<int64_t>(device_cu_count()));
+  hipLaunchKernelGGL(glu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, x, ldx, y, ldy, n, rows, op,
+                     swapped);
   return launch_status();
 }
 

@@ -1,8 +1,8 @@
 """ctypes mirror of the ggml-backend-shaped surface (include/spiral_ggml.h).
 
 Tensors, graphs, buffers and the backend as a llama.cpp-side shim would use
-them: build op nodes with mul_mat / get_rows / mul_mat_id (the ggml builder
-names), place tensors in a Buffer, upload canonical GGUF bytes with
+them: build op nodes with mul_mat / get_rows / mul_mat_id / glu (the ggml
+builder names), place tensors in a Buffer, upload canonical GGUF bytes with
 Buffer.set, and run a graph on a Backend. All compute happens in
 libspiral_quants.so on the device; nothing here computes.
 """
@@ -12,9 +12,12 @@ import ctypes
 from ._lib import (TYPE_BF16, TYPE_F16, TYPE_F32, TYPE_I32, TYPE_Q4_0, TYPE_Q6_K, TYPE_Q8_0,  # noqa: F401
                    check, lib)
 
-MAX_DIMS, MAX_SRC, MAX_NAME = 4, 10, 64
+MAX_DIMS, MAX_SRC, MAX_NAME, MAX_OP_PARAMS = 4, 10, 64, 16
 (OP_NONE, OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_VIEW, OP_RESHAPE, OP_PERMUTE,
- OP_TRANSPOSE) = range(8)
+ OP_TRANSPOSE, OP_GLU) = range(9)
+# ggml GLU variants (op_params[0] of a GLU node; ggml_glu_op numbering)
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = range(6)
+FLAG_OUTPUT = 2  # ggml GGML_TENSOR_FLAG_OUTPUT
 
 # bytes per block and elements per block (ggml type traits)
 TYPE_TRAITS = {
@@ -33,6 +36,8 @@ Tensor._fields_ = [
     ("ne", ctypes.c_int64 * MAX_DIMS),
     ("nb", ctypes.c_size_t * MAX_DIMS),
     ("op", ctypes.c_int32),
+    ("op_params", ctypes.c_int32 * MAX_OP_PARAMS),
+    ("flags", ctypes.c_int32),
     ("src", ctypes.POINTER(Tensor) * MAX_SRC),
     ("data", ctypes.c_void_p),
     ("name", ctypes.c_char * MAX_NAME),
@@ -129,6 +134,14 @@ def get_rows(a, ids, out_type=TYPE_F32, name="get_rows"):
 def mul_mat_id(a, b, ids, name="mul_mat_id"):
     """ggml_mul_mat_id(as, b, ids): [as.ne1, ids.ne0, ids.ne1] F32."""
     return _node(TYPE_F32, [a.ne[1], ids.ne[0], ids.ne[1], 1], OP_MUL_MAT_ID, [a, b, ids], name)
+
+
+def glu(a, op=GLU_SWIGLU, swapped=False, name="glu"):
+    """ggml_glu(a, op, swapped) (single-tensor form): [a.ne0 / 2, a.ne1, ...] F32."""
+    t = _node(TYPE_F32, [a.ne[0] // 2, a.ne[1], a.ne[2], a.ne[3]], OP_GLU, [a], name)
+    t.op_params[0] = op
+    t.op_params[1] = int(swapped)
+    return t
 
 
 def supports_op(t):

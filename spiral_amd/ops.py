@@ -119,6 +119,45 @@ def mul_mat_id(qtype, w, expert_stride, n_expert, n_rows, k, x, ids, out_dtype=t
     return out
 
 
+# ggml GLU variants (ggml_glu_op numbering); SWIGLU_OAI (3) is not implemented.
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = range(6)
+
+
+def mul_mat_id_glu(qtype, w, expert_stride, n_expert, n_rows, k, x, ids, glu_op=GLU_SWIGLU, swapped=False,
+                   out_dtype=torch.bfloat16, workspace=None, out=None):
+    """MUL_MAT_ID + GLU in one pass: W rows [0, F) gate, [F, 2F) up (n_rows =
+    2F); y[t, s, f] = act(gate) * up (act(up) * gate when swapped), y
+    [n_tokens, top_k, F]."""
+    _require_cuda(w, x, ids)
+    n_tokens, top_k = ids.shape
+    x_slots = x.shape[1]
+    ids = ids.to(torch.int32).contiguous()
+    x = x.contiguous()
+    if workspace is None:
+        workspace = mul_mat_id_workspace(n_expert, n_tokens, top_k, w.device)
+    if out is None:
+        out = torch.empty((n_tokens, top_k, n_rows // 2), dtype=out_dtype, device=w.device)
+    check(lib().spiral_mul_mat_id_glu(qtype, _ptr(w), expert_stride, n_expert, n_rows, k, _ptr(x), x_slots,
+                                      _ptr(ids), n_tokens, top_k, glu_op, int(swapped), _ptr(out),
+                                      _out_type(out.dtype), _ptr(workspace), workspace.numel(), _stream()),
+          "mul_mat_id_glu")
+    return out
+
+
+def glu(x, glu_op=GLU_SWIGLU, swapped=False, out=None):
+    """ggml GLU over the last dimension of a float32 tensor [..., 2F] -> [..., F]."""
+    _require_cuda(x)
+    if x.dtype != torch.float32:
+        raise TypeError("glu takes float32")
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    F = x2.shape[1] // 2
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (F,), dtype=torch.float32, device=x.device)
+    check(lib().spiral_glu(glu_op, int(swapped), _ptr(x2), x2.shape[1], F, x2.shape[0], _ptr(out), F, _stream()),
+          "glu")
+    return out
+
+
 def unpack_all(qtype, packed, weights_rows, weights_cols):
     """quants_unpack_all over reference records -> bf16 in reference order."""
     _require_cuda(packed)

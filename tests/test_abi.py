@@ -147,7 +147,17 @@ def test_validation_before_device_work(spiral_lib):
     assert L.spiral_mul_mat_id(q4, p, 32, 4, 4, 64, p, 3, p, 2, 2, p, _lib.TYPE_F32, p, 1 << 20, None) == 1
     assert L.spiral_mul_mat_id(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, p, _lib.TYPE_F32, p, 4, None) == 7
     assert L.quants_unpack_all(q4, p, 96, 8, p, None) == 1
+    # fused MUL_MAT_ID + GLU: unknown / unimplemented GLU op, bad swapped flag, odd row count
+    assert L.spiral_mul_mat_id_glu(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, 3, 0, p, _lib.TYPE_F32, p, 1 << 20, None) == 6
+    assert L.spiral_mul_mat_id_glu(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, 2, 2, p, _lib.TYPE_F32, p, 1 << 20, None) == 6
+    assert L.spiral_mul_mat_id_glu(q4, p, 144, 4, 5, 64, p, 1, p, 2, 2, 2, 0, p, _lib.TYPE_F32, p, 1 << 20, None) == 1
+    assert L.spiral_glu(7, 0, p, 8, 4, 2, p, 4, None) == 6
+    assert L.spiral_glu(2, 0, p, 7, 4, 2, p, 4, None) == 1  # ldx < 2F
+    assert L.spiral_glu(2, 0, p, 8, 4, 0, p, 4, None) == 0  # no rows: a no-op
     if L.spiral_device_count() == 0:
+        assert L.spiral_mul_mat_id_glu(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, 2, 0, p, _lib.TYPE_F32, p, 1 << 20,
+                                       None) == 4
+        assert L.spiral_glu(2, 1, p, 8, 4, 2, p, 4, None) == 4
         assert L.spiral_dequant_bf16(q4, p, 4, 64, p, 64, None) == 4
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 1, p, _lib.TYPE_F32, 4, None, 0, None) == 4
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, p, 8192, None) == 4

@@ -5,7 +5,8 @@ graph_compute, compare with a CPU reference (here the oracle).
 CPU tests: tensor sizes, supports_op's refusals, and that nothing pretends to
 work without a device. GPU tests: canonical-bytes set/get round trips through
 the planar device layout (whole matrices and arbitrary byte ranges), and
-MUL_MAT / GET_ROWS / MUL_MAT_ID nodes against the oracle.
+MUL_MAT / GET_ROWS / MUL_MAT_ID / GLU nodes (and MUL_MAT_ID fused with the
+GLU over it) against the oracle.
 """
 
 import ctypes
@@ -73,6 +74,27 @@ def test_supports_op_refusals(spiral_lib):
         v = ggml.new_tensor(ggml.TYPE_F32, [4])
         v.op = op
         assert ggml.supports_op(v)
+
+
+def test_supports_op_glu(spiral_lib):
+    """GLU nodes: the single-tensor form over F32 rows with a known variant."""
+    h = ggml.new_tensor(ggml.TYPE_F32, [192, 3, 5])
+    for op in (ggml.GLU_REGLU, ggml.GLU_GEGLU, ggml.GLU_SWIGLU, ggml.GLU_GEGLU_ERF, ggml.GLU_GEGLU_QUICK):
+        for swapped in (False, True):
+            g = ggml.glu(h, op, swapped)
+            assert list(g.ne) == [96, 3, 5, 1]
+            assert ggml.supports_op(g)
+    assert not ggml.supports_op(ggml.glu(h, ggml.GLU_SWIGLU_OAI))  # float parameters: not implemented
+    g = ggml.glu(h)
+    g.op_params[1] = 2
+    assert not ggml.supports_op(g)
+    g = ggml.glu(h)
+    g.src[1] = ctypes.pointer(h)  # the split form (separate gate and up tensors)
+    assert not ggml.supports_op(g)
+    assert not ggml.supports_op(ggml.glu(ggml.new_tensor(ggml.TYPE_BF16, [192, 3])))
+    g = ggml.glu(h)
+    g.ne[0] = 95
+    assert not ggml.supports_op(g)
 
 
 def test_no_device_means_no_backend(spiral_lib):
@@ -227,6 +249,52 @@ def test_mul_mat_id_node(cuda, qtype):
         for s in range(top_k):
             ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], n, k), xb[t][None])[0]
             assert rel_err(y[t, s], ref) <= REL_TOL_EXACT_W
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
+def test_mul_mat_id_then_glu_fused_and_not(cuda):
+    """MUL_MAT_ID followed by GLU over it: graph_compute runs the two as one
+    pass (the product's own data is not written). Flagged OUTPUT, the
+    product is computed and written, and the GLU result is the same bits."""
+    qtype, k, F, n_expert, top_k, n_tokens = O.Q4_0, 128, 48, 5, 2, 9
+    raws = [synth.make_weights(qtype, 2 * F, k, 80 + e) for e in range(n_expert)]
+    rng = np.random.default_rng(9)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    xf = rng.standard_normal((n_tokens, 1, k), dtype=np.float32)
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, 2 * F, n_expert]))
+    buf.set(a, np.concatenate(raws).tobytes())
+    b = buf.alloc(ggml.new_tensor(ggml.TYPE_F32, [k, 1, n_tokens]))
+    buf.set(b, xf.tobytes())
+    it = buf.alloc(ggml.new_tensor(ggml.TYPE_I32, [top_k, n_tokens]))
+    buf.set(it, ids.tobytes())
+    prod = buf.alloc(ggml.mul_mat_id(a, b, it))
+    g = buf.alloc(ggml.glu(prod, ggml.GLU_SWIGLU))
+    assert ggml.supports_op(g)
+    sentinel = np.full(2 * F * top_k * n_tokens, 7.0, dtype=np.float32).tobytes()
+    buf.set(prod, sentinel)
+    be = ggml.Backend(0)
+    assert be.graph_compute([prod, g]) == 0
+    be.synchronize()
+    assert buf.get(prod) == sentinel  # fused: the product was never written
+    y = np.frombuffer(buf.get(g), dtype=np.float32).reshape(n_tokens, top_k, F)
+    xb = synth.bf16_bits(xf[:, 0])
+    for t in range(n_tokens):
+        for s in range(top_k):
+            p_ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], 2 * F, k), xb[t][None])[0]
+            assert rel_err(y[t, s], O.glu_f64(p_ref, O.GLU_SWIGLU)) <= REL_TOL
+    prod.flags = ggml.FLAG_OUTPUT
+    assert be.graph_compute([prod, g]) == 0
+    be.synchronize()
+    assert buf.get(prod) != sentinel
+    p = np.frombuffer(buf.get(prod), dtype=np.float32).reshape(n_tokens, top_k, 2 * F)
+    assert np.frombuffer(buf.get(g), dtype=np.float32).reshape(n_tokens, top_k, F).tobytes() == y.tobytes()
+    for t in range(n_tokens):
+        for s in range(top_k):
+            p_ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], 2 * F, k), xb[t][None])[0]
+            assert rel_err(p[t, s], p_ref) <= REL_TOL_EXACT_W
     be.free()
     buf.free()
 

@@ -255,7 +255,8 @@ def test_gemm_q4_0_prefill_512x4096x4096(cuda):
 
 # ---- MoE grouped GEMM -----------------------------------------------------------
 
-def _moe_case(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, out_dtype, ids=None):
+def _moe_inputs(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, ids=None):
+    """Seeded expert weights (canonical and planar on the device), ids, x."""
     rng = np.random.default_rng(seed)
     per = O.row_bytes(qtype, k) * n
     raws = [synth.make_weights(qtype, n, k, seed * 1000 + e) for e in range(n_expert)]
@@ -265,6 +266,28 @@ def _moe_case(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, out_d
     if ids is None:
         ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
     x = synth.make_x(n_tokens * x_slots, k, seed + 7).reshape(n_tokens, x_slots, k)
+    return w, per, raws, ids, x
+
+
+def _moe_ref(qtype, raws, n, k, ids, x):
+    """The oracle's [n_tokens][top_k][n] product (zero rows for ids routed nowhere)."""
+    n_tokens, top_k = ids.shape
+    n_expert = len(raws)
+    deq = {}
+    ref = np.zeros((n_tokens, top_k, n))
+    for t in range(n_tokens):
+        for s in range(top_k):
+            e = ids[t, s]
+            if e < 0 or e >= n_expert:
+                continue
+            if e not in deq:
+                deq[e] = O.dequant(qtype, raws[e], n, k)
+            ref[t, s] = O.matmul_f64(deq[e], x[t, s % x.shape[1]][None, :])[0]
+    return ref
+
+
+def _moe_case(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, out_dtype, ids=None):
+    w, per, raws, ids, x = _moe_inputs(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, ids)
     y = ops.mul_mat_id(qtype, w, per, n_expert, n, k, dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda),
                        out_dtype=out_dtype)
     torch.cuda.synchronize()
@@ -399,3 +422,87 @@ def test_ref_unpack_mmul_all(cuda, qtype):
     ref = O.matmul_f64(w, synth.bf16_bits(inputs_rows))  # [4, cols]
     ref_tiled = ref.reshape(4, cols // 8, 8).transpose(1, 0, 2).reshape(-1)
     assert rel_err(out, ref_tiled) <= REL_TOL_EXACT_W
+
+
+# ---- MUL_MAT_ID fused with GLU -------------------------------------------------
+
+GLU_OPS = [ops.GLU_REGLU, ops.GLU_GEGLU, ops.GLU_SWIGLU, ops.GLU_GEGLU_ERF, ops.GLU_GEGLU_QUICK]
+
+
+def test_glu_standalone(cuda):
+    """ggml GLU on its own (float32 in and out) against the oracle's float64
+    restatement, every variant, both half orders."""
+    rng = np.random.default_rng(21)
+    h = (3.0 * rng.standard_normal((7, 3, 2 * 50))).astype(np.float32)
+    ht = torch.from_numpy(h).to(cuda)
+    for op in GLU_OPS:
+        for swapped in (False, True):
+            y = ops.glu(ht, op, swapped).cpu().numpy()
+            err = rel_err(y, O.glu_f64(h, op, swapped))
+            assert err <= 1e-5, (op, swapped, err)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_mul_mat_id_glu_matches_unfused_and_oracle(cuda, qtype):
+    """The fused pass sums every (pair, row) exactly as MUL_MAT_ID does, so it
+    equals MUL_MAT_ID followed by the standalone GLU bit for bit (F32 out;
+    BF16 out is that value rounded), and the oracle's product through its
+    GLU within the product bar. F = 72 is not a whole number of 16-row
+    groups; 40 tokens x top-3 over 8 experts gives 16+ pairs per expert."""
+    k = O.BLOCK_ELEMS[qtype] * (2 if qtype == O.Q6_K else 8)
+    n_expert, F, n_tokens, top_k = 8, 72, 40, 3
+    w, per, raws, ids, x = _moe_inputs(cuda, qtype, n_expert, 2 * F, k, n_tokens, top_k, 1, 31)
+    xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
+    prod = ops.mul_mat_id(qtype, w, per, n_expert, 2 * F, k, xd, idd, out_dtype=torch.float32)
+    ref_prod = _moe_ref(qtype, raws, 2 * F, k, ids, x)
+    for op in GLU_OPS:
+        for swapped in (False, True):
+            fused = ops.mul_mat_id_glu(qtype, w, per, n_expert, 2 * F, k, xd, idd, op, swapped,
+                                       out_dtype=torch.float32)
+            unfused = ops.glu(prod, op, swapped)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, unfused), (op, swapped)
+            err = rel_err(fused.cpu().numpy(), O.glu_f64(ref_prod, op, swapped))
+            assert err <= REL_TOL, (op, swapped, err)
+    fb = ops.mul_mat_id_glu(qtype, w, per, n_expert, 2 * F, k, xd, idd, ops.GLU_SWIGLU, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(fb, ops.glu(prod, ops.GLU_SWIGLU).to(torch.bfloat16))
+
+
+def test_mul_mat_id_glu_routing_paths_and_bad_ids(cuda):
+    """Both routing paths (scan inside the kernel; counting-sort kernel above
+    1024 pairs) with ids routed nowhere: those rows are zero over the F
+    output columns, the others equal the unfused chain."""
+    qtype, F, k = O.Q4_0, 40, 256
+    for n_expert, n_tokens, top_k in ((6, 30, 2), (12, 160, 8)):
+        rng = np.random.default_rng(n_tokens)
+        ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+        ids[::7, 0] = -1
+        ids[3::11, -1] = 99
+        w, per, raws, ids, x = _moe_inputs(cuda, qtype, n_expert, 2 * F, k, n_tokens, top_k, 1, 32, ids)
+        xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
+        out = torch.full((n_tokens, top_k, F), 7.0, device=cuda)
+        ops.mul_mat_id_glu(qtype, w, per, n_expert, 2 * F, k, xd, idd, ops.GLU_GEGLU, out=out)
+        prod = ops.mul_mat_id(qtype, w, per, n_expert, 2 * F, k, xd, idd, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ops.glu(prod, ops.GLU_GEGLU))
+        bad = (ids < 0) | (ids >= n_expert)
+        assert not out.cpu().numpy()[bad].any()
+
+
+def test_mul_mat_id_glu_moe_workload_shape(cuda):
+    """The MoE workload's gate_up stage (128 experts of 1536 x 2048 Q4_0, 64
+    tokens, top-8) fused with SwiGLU: [64][8][768] bf16, the down stage's input."""
+    qtype, n_expert, n, k, n_tokens, top_k = O.Q4_0, 128, 1536, 2048, 64, 8
+    w, per, raws, ids, x = _moe_inputs(cuda, qtype, n_expert, n, k, n_tokens, top_k, 1, 13)
+    xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
+    fused = ops.mul_mat_id_glu(qtype, w, per, n_expert, n, k, xd, idd, ops.GLU_SWIGLU, out_dtype=torch.bfloat16)
+    prod = ops.mul_mat_id(qtype, w, per, n_expert, n, k, xd, idd, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert fused.shape == (n_tokens, top_k, n // 2)
+    assert torch.equal(fused, ops.glu(prod, ops.GLU_SWIGLU).to(torch.bfloat16))
+    sel = [(t, s) for t in range(0, n_tokens, 9) for s in (0, top_k - 1)]
+    ref = np.stack([O.glu_f64(O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], n, k), x[t, 0][None, :])[0],
+                              ops.GLU_SWIGLU) for t, s in sel])
+    got = np.stack([fused[t, s].float().cpu().numpy() for t, s in sel])
+    assert rel_err(got, ref) <= REL_TOL

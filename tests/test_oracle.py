@@ -19,6 +19,8 @@ import json
 from fractions import Fraction
 from pathlib import Path
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -340,3 +342,29 @@ def test_quant_matmul_matches_dequant_then_matmul(oracle, qtype):
     ref = O.matmul_f64(w, x)
     got = O.quant_matmul_f32(qtype, raw, n, k, x, threads=2)
     assert np.allclose(got, ref, rtol=1e-4, atol=1e-3 * np.abs(ref).max())
+
+
+def test_glu_oracle_closed_forms():
+    """The GLU restatement against values the mathematics fixes: relu, silu
+    and the logistic at known points, gelu(1) = Phi(1), the tanh form within
+    its published 1e-3 of the erf form, x * act at 0, and swapped = the
+    halves exchanged (a wrong half or sign fails one of these)."""
+    a = np.array([-2.0, -0.5, 0.0, 1.0, 3.0])
+    b = np.array([1.0, 2.0, -1.0, 0.5, -2.0])
+    h = np.concatenate([a, b])
+    assert np.array_equal(O.glu_f64(h, O.GLU_REGLU), np.array([0.0, 0.0, 0.0, 0.5, -6.0]))
+    sig1 = 1.0 / (1.0 + math.exp(-1.0))
+    assert math.isclose(O.glu_f64(np.array([1.0, 1.0]), O.GLU_SWIGLU)[0], sig1, rel_tol=1e-15)
+    assert math.isclose(O.glu_f64(np.array([1.0, 1.0]), O.GLU_GEGLU_ERF)[0], 0.8413447460685429, rel_tol=1e-14)
+    assert math.isclose(O.glu_f64(np.array([1.0, 1.0]), O.GLU_GEGLU_QUICK)[0], 1.0 / (1.0 + math.exp(-1.702)),
+                        rel_tol=1e-15)
+    xs = np.linspace(-4.0, 4.0, 801)
+    ones = np.ones_like(xs)
+    tanh_form = O.glu_f64(np.concatenate([xs, ones]), O.GLU_GEGLU)
+    erf_form = O.glu_f64(np.concatenate([xs, ones]), O.GLU_GEGLU_ERF)
+    assert np.max(np.abs(tanh_form - erf_form)) < 1e-3
+    silu = O.glu_f64(np.concatenate([xs, ones]), O.GLU_SWIGLU)
+    assert np.allclose(silu, xs / (1.0 + np.exp(-xs)), rtol=1e-15)
+    for op in (O.GLU_REGLU, O.GLU_GEGLU, O.GLU_SWIGLU, O.GLU_GEGLU_ERF, O.GLU_GEGLU_QUICK):
+        assert O.glu_f64(np.array([0.0, 5.0]), op)[0] == 0.0
+        assert np.array_equal(O.glu_f64(h, op, swapped=True), O.glu_f64(np.concatenate([b, a]), op))
