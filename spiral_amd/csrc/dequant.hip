@@ -10,7 +10,8 @@
 // (v_cvt_pk_bf16_f32, round-to-nearest-even) gives the same bits.
 //
 // Work item: one group of 8 consecutive output elements of one row, written
-// as one 16-byte store, so consecutive lanes store consecutive 16 bytes.
+// as one 16-byte non-temporal store, so consecutive lanes store consecutive
+// 16 bytes and the output streams to memory without occupying L2.
 // Grids larger than 2^32 - 1 workgroups, or rows longer than 2^32 - 1 groups,
 // are rejected with SPIRAL_ERR_SHAPE.
 #include "common.h"
@@ -45,7 +46,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* __restrict_
     o.y = pack_bf16x2(v[h][2], v[h][3]);
     o.z = pack_bf16x2(v[h][4], v[h][5]);
     o.w = pack_bf16x2(v[h][6], v[h][7]);
-    *reinterpret_cast<uint4*>(out + row * ld_out + 8 * (h ? g1 : g0)) = o;
+    store_stream16(out + row * ld_out + 8 * (h ? g1 : g0), o);
   }
 }
 
@@ -72,11 +73,11 @@ __global__ void __launch_bounds__(256) get_rows_kernel(const uint8_t* __restrict
   o.w = pack_bf16x2(v[6], v[7]);
   if constexpr (F32_OUT) {
     // The F32 output carries the same exact bf16 values, widened.
-    float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + r * ld_out + 8 * g);
-    p[0] = make_float4(bf16_lo(o.x), bf16_hi(o.x), bf16_lo(o.y), bf16_hi(o.y));
-    p[1] = make_float4(bf16_lo(o.z), bf16_hi(o.z), bf16_lo(o.w), bf16_hi(o.w));
+    float* p = static_cast<float*>(out) + r * ld_out + 8 * g;
+    store_stream16(p, make_uint4(o.x << 16, o.x & 0xffff0000u, o.y << 16, o.y & 0xffff0000u));
+    store_stream16(p + 4, make_uint4(o.z << 16, o.z & 0xffff0000u, o.w << 16, o.w & 0xffff0000u));
   } else {
-    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + r * ld_out + 8 * g) = o;
+    store_stream16(static_cast<uint16_t*>(out) + r * ld_out + 8 * g, o);
   }
 }
 
