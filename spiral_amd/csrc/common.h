@@ -147,4 +147,8 @@ int device_cu_count();
 // the query fails).
 int blocks_per_cu(const void* kernel, int threads, int64_t lds);
 
+// Raises `kernel`'s dynamic-LDS limit to `bytes` on the current device
+// (hipFuncSetAttribute once per device and kernel, thread-safe).
+int allow_dynamic_lds(const void* kernel, int bytes);
+
 }  // namespace spiral

@@ -73,6 +73,29 @@ int blocks_per_cu(const void* kernel, int threads, int64_t lds) {
   return n;
 }
 
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per device and kernel (the attribute is per device; the set is guarded so
+// concurrent first launches from several threads are safe).
+int allow_dynamic_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, std::vector<int>> done;  // kernel -> limit set, by device
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return SPIRAL_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  std::vector<int>& v = done[kernel];
+  if (dev >= static_cast<int>(v.size())) v.resize(dev + 1, 0);
+  if (v[dev] >= bytes) return SPIRAL_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return SPIRAL_ERR_HIP;
+  }
+  v[dev] = bytes;
+  return SPIRAL_OK;
+}
+
 namespace {
 
 __device__ __forceinline__ uint32_t u16x2(const uint16_t* p) {

@@ -995,15 +995,8 @@ int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_
                   const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, hipStream_t s) {
   const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU>;
   const int64_t lds = stream_lds_bytes(k);
-  static bool attr_set = false;  // benign race: every caller sets the same value
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(stream_lds_bytes(kStreamMaxK))) != hipSuccess) {
-      (void)hipGetLastError();
-      return SPIRAL_ERR_HIP;
-    }
-    attr_set = true;
-  }
+  const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), static_cast<int>(stream_lds_bytes(kStreamMaxK)));
+  if (rc != SPIRAL_OK) return rc;
   // About two workgroups per CU in all, each over a contiguous range of
   // whole 16-row groups of one expert (GLU: of its output features).
   const int64_t feat = GLU ? n_rows / 2 : n_rows;
@@ -1241,15 +1234,8 @@ template <int TYPE, bool F32_OUT, bool WINDOWS>
 int launch_skinny(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
                   int64_t ldy, const SkinnyShape& sh, hipStream_t s) {
   const auto kern = skinny_kernel<TYPE, F32_OUT, WINDOWS>;
-  static bool attr_set = false;  // benign race: every caller sets the same value
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(kSkinnyLds)) != hipSuccess) {
-      (void)hipGetLastError();
-      return SPIRAL_ERR_HIP;
-    }
-    attr_set = true;
-  }
+  const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), static_cast<int>(kSkinnyLds));
+  if (rc != SPIRAL_OK) return rc;
   const int64_t n_blocks = ceil_div(sh.groups, kSkinnyWaves / sh.parts);
   const int64_t resident =
       static_cast<int64_t>(device_cu_count()) * blocks_per_cu(reinterpret_cast<const void*>(kern), kSkinnyThreads, sh.lds);
