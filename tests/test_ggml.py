@@ -300,6 +300,46 @@ def test_mul_mat_id_then_glu_fused_and_not(cuda):
 
 
 @pytest.mark.gpu
+def test_mul_mat_id_then_glu_past_the_fused_shapes(cuda):
+    """k > 4096: the fused pass is refused (SPIRAL_ERR_SHAPE), and
+    graph_compute runs MUL_MAT_ID (its non-streaming kernel) and then the
+    standalone GLU, with the same result as the oracle."""
+    import torch
+    from spiral_amd import ops
+
+    qtype, k, F, n_expert, top_k, n_tokens = O.Q4_0, 4096 + 256, 24, 3, 2, 5
+    raws = [synth.make_weights(qtype, 2 * F, k, 90 + e) for e in range(n_expert)]
+    rng = np.random.default_rng(10)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    xf = rng.standard_normal((n_tokens, 1, k), dtype=np.float32)
+    per = O.row_bytes(qtype, k) * 2 * F
+    w = torch.cat([ops.to_planar(qtype, torch.from_numpy(r).to(cuda), 2 * F, k) for r in raws])
+    xb = synth.bf16_bits(xf[:, 0])
+    xd = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16).to(cuda).view(n_tokens, 1, k)
+    with pytest.raises(RuntimeError, match="SHAPE"):
+        ops.mul_mat_id_glu(qtype, w, per, n_expert, 2 * F, k, xd, torch.from_numpy(ids).to(cuda), ops.GLU_GEGLU_ERF)
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, 2 * F, n_expert]))
+    buf.set(a, np.concatenate(raws).tobytes())
+    b = buf.alloc(ggml.new_tensor(ggml.TYPE_F32, [k, 1, n_tokens]))
+    buf.set(b, xf.tobytes())
+    it = buf.alloc(ggml.new_tensor(ggml.TYPE_I32, [top_k, n_tokens]))
+    buf.set(it, ids.tobytes())
+    prod = buf.alloc(ggml.mul_mat_id(a, b, it))
+    g = buf.alloc(ggml.glu(prod, ggml.GLU_GEGLU_ERF, swapped=True))
+    be = ggml.Backend(0)
+    assert be.graph_compute([prod, g]) == 0
+    be.synchronize()
+    y = np.frombuffer(buf.get(g), dtype=np.float32).reshape(n_tokens, top_k, F)
+    for t in range(n_tokens):
+        for s in range(top_k):
+            p_ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], 2 * F, k), xb[t][None])[0]
+            assert rel_err(y[t, s], O.glu_f64(p_ref, O.GLU_GEGLU_ERF, swapped=True)) <= REL_TOL
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
 def test_graph_of_several_nodes_and_refusal(cuda):
     qtype, k, n = O.Q4_0, 128, 32
     raw = synth.make_weights(qtype, n, k, 70)
