@@ -31,10 +31,13 @@
 //      - Scheduling fences keep each step's MFMAs, LDS reads, dequantization
 //        and loads together; without them the compiler hoists later steps'
 //        dequantization above the loads it waits for.
-//      - The four k-quarters are summed through LDS at the end.
+//      - The four k-quarters are summed through LDS at the end; each wave
+//        then stages its 16 x 64 output block in LDS and writes it as 16-byte
+//        row pieces (1.7 us faster than per-element stores at M = 512).
 //  Workgroups are numbered so that each XCD (dispatch is round-robin over the
 //  8 XCDs) gets a contiguous range of tiles sharing X rows in its L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "dequant_impl.h"
@@ -283,19 +286,36 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const uint8_t* __restric
       for (int e = 0; e < 4; ++e) out[j][e] += src[(j * 4 + e) * 64 + lane];
   }
 
-  // Accumulator layout: lane l holds D[4 (l / 16) + e][l % 16], e < 4.
+  // The wave's 16 x 64 output block goes through LDS (accumulator layout:
+  // lane l holds D[4 (l / 16) + e][16 j + l % 16]) so that it leaves as
+  // 16-byte row pieces instead of 2- or 4-byte scattered stores. Each wave
+  // uses its own region, after every wave has read the partials above.
+  using OutT = typename std::conditional<F32_OUT, float, __bf16>::type;
+  constexpr int kPer = 16 / sizeof(OutT);           // elements per 16-byte piece
+  constexpr int kTPitch = 64 + kPer;                // padded row, in elements
+  __syncthreads();
+  OutT* T = reinterpret_cast<OutT*>(smem) + wave * 16 * kTPitch;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t gn = n0 + 16 * j + (lane & 15);
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t gm = row0 + 16 * q + 4 * (lane >> 4) + e;
-      if (gm < m && gn < n_rows) {
-        if constexpr (F32_OUT)
-          static_cast<float*>(y)[gm * ldy + gn] = out[j][e];
-        else
-          static_cast<__bf16*>(y)[gm * ldy + gn] = static_cast<__bf16>(out[j][e]);
-      }
+    for (int e = 0; e < 4; ++e) T[(4 * (lane >> 4) + e) * kTPitch + 16 * j + (lane & 15)] = static_cast<OutT>(out[j][e]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  constexpr int kPieces = 16 * 64 / kPer;           // per wave: 128 (bf16) or 256 (f32)
+#pragma unroll
+  for (int h = 0; h < kPieces / 64; ++h) {
+    const int c = lane + 64 * h;
+    const int r = c / (64 / kPer), col = (c % (64 / kPer)) * kPer;
+    const int64_t gm = row0 + 16 * q + r, gn = n0 + col;
+    if (gm >= m) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(T + r * kTPitch + col);
+    OutT* dst = static_cast<OutT*>(y) + gm * ldy + gn;
+    if (gn + kPer <= n_rows && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const OutT* src = T + r * kTPitch + col;
+      for (int i = 0; i < kPer && gn + i < n_rows; ++i) dst[i] = src[i];
     }
   }
 }
