@@ -162,6 +162,19 @@ def test_gemv_small(cuda, qtype, out_dtype):
             assert rel_err(y, ref_u) <= REL_TOL_UNROUNDED_W, (n, rel_err(y, ref_u))
 
 
+@pytest.mark.parametrize("k_blocks", [17, 65, 127, 129, 192, 257])
+def test_gemv_q8_0_scale_spans(cuda, k_blocks):
+    """The Q8_0 GEMV loads a unit's scales one dword per lane and spreads
+    them across lanes: rows with an odd number of blocks start in the upper
+    half of a dword on odd rows (37 rows), one pass in registers (17: one
+    task per lane, 65 and 127: four) or several passes (129 and 257: a
+    128-scale span can cover 65 dwords; 192: even)."""
+    k = 32 * k_blocks
+    y, ref, ref_u = _mul_mat_case(cuda, O.Q8_0, 37, k, 1, 40 + k_blocks, torch.float32, unrounded=True)
+    assert rel_err(y, ref) <= REL_TOL, rel_err(y, ref)
+    assert rel_err(y, ref_u) <= REL_TOL_UNROUNDED_W, rel_err(y, ref_u)
+
+
 @pytest.mark.parametrize("qtype,n,k", [(O.Q8_0, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q4_0, 4096, 4096)])
 def test_gemv_workload_shapes(cuda, qtype, n, k):
     y, ref = _mul_mat_case(cuda, qtype, n, k, 1, 3, torch.bfloat16)
