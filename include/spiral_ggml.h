@@ -10,7 +10,8 @@
  * repack header is meant to be compiled into that loader
  * (src/quants/common/repack.h:5-7). ggml itself is not vendored. The types
  * below therefore mirror the public ggml-backend interface field for field
- * (ggml_tensor's type / buffer / ne / nb / op / op_params / flags / src / data / name, ggml_cgraph's
+ * (ggml_tensor's type / buffer / ne / nb / op / op_params / flags / src /
+ * view_src / view_offs / data / name, ggml_cgraph's
  * n_nodes / nodes, ggml_backend_buffer_i's alloc / free / get_base /
  * init_tensor / set_tensor / get_tensor / memset_tensor / clear,
  * ggml_backend_i's graph_compute / synchronize, ggml_backend_device_i's
@@ -68,8 +69,17 @@ typedef struct spiral_backend spiral_backend; /* one device + stream (opaque) */
 
 /* ggml_tensor's fields that a backend reads: type (SPIRAL_TYPE_*, the ggml
  * type ids), ne (elements per dimension, ne[0] innermost), nb (byte strides),
- * op, op_params and flags, src (the node's inputs), data (device address
- * inside `buffer`). */
+ * op, op_params and flags, src (the node's inputs), view_src / view_offs (for
+ * a view: the tensor that owns the memory, never itself a view, and the
+ * view's byte offset into it; NULL / 0 otherwise), data (device address
+ * inside `buffer`).
+ *
+ * A quantized view is usable (as MUL_MAT / GET_ROWS / MUL_MAT_ID src0, or by
+ * set_tensor / get_tensor) only when it starts whole planar matrices of its
+ * source: same row length and row count as the source's matrices, and an
+ * offset that is a whole number of them (for example one expert of a stack).
+ * A row-range view inside a matrix is refused: the planar layout is relative
+ * to each matrix's start, so its rows are not where the view's data points. */
 typedef struct spiral_tensor {
   int32_t type;
   spiral_buffer* buffer;
@@ -79,6 +89,8 @@ typedef struct spiral_tensor {
   int32_t op_params[SPIRAL_MAX_OP_PARAMS];
   int32_t flags;
   struct spiral_tensor* src[SPIRAL_MAX_SRC];
+  struct spiral_tensor* view_src;
+  size_t view_offs;
   void* data;
   char name[SPIRAL_MAX_NAME];
 } spiral_tensor;
@@ -160,8 +172,12 @@ void* spiral_backend_stream(const spiral_backend* be);
  * MUL_MAT_ID routing lists) is owned by the backend and grows on demand.
  * A MUL_MAT_ID node followed by a GLU node over it runs as one fused pass
  * (spiral_mul_mat_id_glu) when no other node reads the MUL_MAT_ID result,
- * it is not flagged OUTPUT and k <= 4096; its own data is then not written,
- * as with ggml's fusion. Asynchronous: returns when the work is queued. */
+ * it is not flagged OUTPUT, the GLU output is contiguous and
+ * spiral_mul_mat_id_glu_fits() holds for its shape; the MUL_MAT_ID's own data
+ * is then not written, as with ggml's fusion. Only the graph passed in is
+ * searched for other readers: a caller that splits a model graph (ggml's
+ * scheduler) must flag OUTPUT every MUL_MAT_ID result read in another split.
+ * Asynchronous: returns when the work is queued. */
 int spiral_backend_graph_compute(spiral_backend* be, const spiral_cgraph* graph);
 /* Waits for the backend's stream (ggml synchronize). */
 int spiral_backend_synchronize(spiral_backend* be);

@@ -14,8 +14,9 @@
  *    the reference's weights_cols) of k elements (ggml ne0, the reference's
  *    weights_rows). A product computes y[i][n] = sum_k x[i][k] * W[n][k].
  *  - bf16 values travel as uint16_t bit patterns.
- *  - Thread-safe for calls on distinct streams; the library keeps no mutable
- *    global state.
+ *  - Thread-safe for calls on distinct streams. Process-wide state: per-device
+ *    caches (compute-unit counts, occupancy, raised LDS limits) filled once
+ *    under a lock, and the repack warning route (quants_set_repack_warn).
  */
 #ifndef SPIRAL_QUANTS_H
 #define SPIRAL_QUANTS_H
@@ -66,8 +67,18 @@ int spiral_device_count(void);
  * which the reference builds once per format; here the format is part of  *
  * the name. Host memory; the output is the reference's record stream,     *
  * byte for byte. A subnormal fp16 scale is stored as +0 and one warning    *
- * line goes to stderr per call (src/quants/common/repack.h:38-61).         *
+ * line per call goes to stderr, or to the callback set below              *
+ * (src/quants/common/repack.h:38-61).                                      *
  * ===================================================================== */
+
+/* Routes the repack warning line: the reference lets a caller that compiles
+ * its header redefine QUANTS_REPACK_WARN to reroute or silence the line
+ * (src/quants/common/repack.h:9-14); a shared library takes a callback.
+ * fn receives the line (ending in a newline) and `user`; fn == NULL restores
+ * stderr; a callback that does nothing silences it. Process-wide; a repack
+ * running while this is called uses either the old or the new route. */
+typedef void (*quants_warn_fn)(const char* line, void* user);
+void quants_set_repack_warn(quants_warn_fn fn, void* user);
 int64_t quants_q4_0_record_count(int64_t weights_rows, int64_t weights_cols);
 int64_t quants_q4_0_packed_bytes(int64_t weights_rows, int64_t weights_cols);
 int64_t quants_q4_0_repack(const uint8_t* src, int64_t src_col_stride_bytes,
@@ -204,9 +215,13 @@ enum {
  * g = (W x)[f], u = (W x)[F + f] (act(u) * g when swapped). y is
  * [n_tokens][top_k][F] of y_type; the [.. ][2F] product is never written.
  * Other arguments as spiral_mul_mat_id. Implemented for the decode shapes
- * (k <= 4096; else SPIRAL_ERR_SHAPE); SPIRAL_ERR_TYPE for an unknown or
+ * (spiral_mul_mat_id_glu_fits; else SPIRAL_ERR_SHAPE); SPIRAL_ERR_TYPE for an unknown or
  * unimplemented glu_op. No counterpart in the reference, whose MoE path is
  * a plan (src/quants/TODO.md:55,214-220). */
+/* 1 when spiral_mul_mat_id_glu implements this expert shape (a quantized
+ * type, n_rows even and positive, k a positive multiple of the block and
+ * within the fused pass's limit, 4096), else 0. Pure host logic. */
+int spiral_mul_mat_id_glu_fits(int type, int64_t n_rows, int64_t k);
 int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride,
                           int64_t n_expert, int64_t n_rows, int64_t k,
                           const uint16_t* x, int64_t x_slots,

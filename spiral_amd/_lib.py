@@ -39,6 +39,7 @@ SIGNATURES = {
     "quants_q6_k_record_count": (_i64, [_i64, _i64]),
     "quants_q6_k_packed_bytes": (_i64, [_i64, _i64]),
     "quants_q6_k_repack": (_i64, [_p, _i64, _p, _i64, _i64, _i64]),
+    "quants_set_repack_warn": (None, [_p, _p]),
     "quants_unpack_all": (_int, [_int, _p, _i64, _i64, _p, _p]),
     "quants_unpack_mmul_all": (_int, [_int, _p, _p, _p, _i64, _i64, _p]),
     "spiral_row_bytes": (_i64, [_int, _i64]),
@@ -52,6 +53,7 @@ SIGNATURES = {
     "spiral_mul_mat_id_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "spiral_mul_mat_id": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,
                                  _p, _i64, _p]),
+    "spiral_mul_mat_id_glu_fits": (_int, [_int, _i64, _i64]),
     "spiral_mul_mat_id_glu": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _int, _int,
                                      _p, _int, _p, _i64, _p]),
     "spiral_glu": (_int, [_int, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),

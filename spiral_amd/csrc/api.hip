@@ -17,6 +17,7 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
         int y_type, int glu_op, int swapped, void* workspace, hipStream_t s);
 int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
         hipStream_t s);
+bool moe_glu_fits_k(int64_t k);
 
 bool glu_op_ok(int op) {
   return op == SPIRAL_GLU_REGLU || op == SPIRAL_GLU_GEGLU || op == SPIRAL_GLU_SWIGLU ||
@@ -99,6 +100,11 @@ int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_
   if (rc != SPIRAL_OK) return rc;
   return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, -1, 0,
              workspace, static_cast<hipStream_t>(stream));
+}
+
+int spiral_mul_mat_id_glu_fits(int type, int64_t n_rows, int64_t k) {
+  if (!is_quant_type(type) || n_rows <= 0 || n_rows % 2 != 0 || k <= 0 || k % block_elems(type) != 0) return 0;
+  return moe_glu_fits_k(k) ? 1 : 0;
 }
 
 int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,

@@ -79,6 +79,22 @@ bool quant_layout_ok(const spiral_tensor* t) {
   return (reinterpret_cast<uintptr_t>(t->data) & 15) == 0;
 }
 
+// A quantized tensor's data must start whole planar matrices: the planar
+// layout is relative to each matrix's start. A view (view_src set; ggml
+// keeps view_src pointing at the tensor that owns the memory) passes only
+// when its matrices are its source's: same row length and row count, at an
+// offset of a whole number of source matrices (one expert of a stack, say).
+// A row-range view inside a matrix fails.
+bool planar_whole(const spiral_tensor* t) {
+  if (!quant_layout_ok(t)) return false;
+  const spiral_tensor* v = t->view_src;
+  if (v == nullptr) return true;
+  if (v->type != t->type || v->ne[0] != t->ne[0] || v->ne[1] != t->ne[1] || !quant_layout_ok(v)) return false;
+  const size_t mat = v->nb[2];
+  if (mat == 0 || t->view_offs % mat != 0) return false;
+  return v->data == nullptr || static_cast<const uint8_t*>(v->data) + t->view_offs == t->data;
+}
+
 // Element tensor with contiguous innermost dimension.
 bool rows_contiguous(const spiral_tensor* t, size_t elem) { return t->nb[0] == elem; }
 
@@ -317,14 +333,17 @@ int compute_glu(spiral_backend* be, const spiral_tensor* t) {
 }
 
 // Node i (MUL_MAT_ID) can run fused with node i + 1 (GLU over it): nothing
-// else in the graph reads node i, it is not a graph output, and the fused
-// pass covers its shape.
+// else in the graph reads node i, it is not a graph output, the fused pass
+// covers its shape, and the GLU output is contiguous (the fused pass writes
+// it as packed [pair][F] rows).
 bool fusable_glu(const spiral_cgraph* graph, int32_t i) {
   if (i + 1 >= graph->n_nodes) return false;
   const spiral_tensor* t = graph->nodes[i];
   const spiral_tensor* g = graph->nodes[i + 1];
   if (t->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU || g->src[0] != t) return false;
-  if ((t->flags & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || t->src[0]->ne[0] > 4096) return false;
+  if ((t->flags & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || !fully_contiguous(g, 4)) return false;
+  const spiral_tensor* a = t->src[0];
+  if (!spiral_mul_mat_id_glu_fits(a->type, a->ne[1], a->ne[0])) return false;
   for (int32_t j = 0; j < graph->n_nodes; ++j) {
     if (j == i + 1) continue;
     for (int s = 0; s < SPIRAL_MAX_SRC; ++s)
@@ -430,7 +449,7 @@ int spiral_buffer_set_tensor(spiral_buffer* buf, spiral_tensor* t, const void* d
   DeviceGuard g(buf->device);
   uint8_t* dst = static_cast<uint8_t*>(t->data);
   if (!is_quant(t)) return hip_rc(hipMemcpy(dst + offset, data, size, hipMemcpyHostToDevice));
-  if (!quant_layout_ok(t)) return SPIRAL_ERR_SHAPE;
+  if (!planar_whole(t)) return SPIRAL_ERR_SHAPE;
   void* stage = nullptr;
   if ((rc = hip_rc(hipMalloc(&stage, size))) != SPIRAL_OK) return rc;
   rc = hip_rc(hipMemcpy(stage, data, size, hipMemcpyHostToDevice));
@@ -462,7 +481,7 @@ int spiral_buffer_get_tensor(spiral_buffer* buf, const spiral_tensor* t, void* d
   DeviceGuard g(buf->device);
   const uint8_t* src = static_cast<const uint8_t*>(t->data);
   if (!is_quant(t)) return hip_rc(hipMemcpy(data, src + offset, size, hipMemcpyDeviceToHost));
-  if (!quant_layout_ok(t)) return SPIRAL_ERR_SHAPE;
+  if (!planar_whole(t)) return SPIRAL_ERR_SHAPE;
   void* stage = nullptr;
   if ((rc = hip_rc(hipMalloc(&stage, size))) != SPIRAL_OK) return rc;
   const int64_t rows = t->ne[1], k = t->ne[0], nb = k / block_elems(t->type);
@@ -489,6 +508,7 @@ int spiral_buffer_memset_tensor(spiral_buffer* buf, spiral_tensor* t, uint8_t va
   DeviceGuard g(buf->device);
   // A constant byte range maps to constant planar bytes only when it covers
   // whole matrices; otherwise scatter it like set_tensor would.
+  if (is_quant(t) && !planar_whole(t)) return SPIRAL_ERR_SHAPE;
   if (is_quant(t) && !(offset % t->nb[2] == 0 && size % t->nb[2] == 0)) {
     uint8_t* host = new (std::nothrow) uint8_t[size];
     if (host == nullptr) return SPIRAL_ERR_CAPACITY;
@@ -520,7 +540,7 @@ int spiral_supports_op(const spiral_tensor* t) {
     case SPIRAL_OP_MUL_MAT: {
       const spiral_tensor* a = t->src[0];
       const spiral_tensor* b = t->src[1];
-      if (a == nullptr || b == nullptr || !is_quant(a) || !quant_layout_ok(a) || !in_spiral_buffer(a)) return 0;
+      if (a == nullptr || b == nullptr || !is_quant(a) || !planar_whole(a) || !in_spiral_buffer(a)) return 0;
       if (!act_type(b->type) || !rows_contiguous(b, elem_size(b->type))) return 0;
       if (t->type != SPIRAL_TYPE_F32 || !rows_contiguous(t, 4)) return 0;
       if (b->ne[0] != a->ne[0] || t->ne[0] != a->ne[1] || t->ne[1] != b->ne[1]) return 0;
@@ -532,7 +552,7 @@ int spiral_supports_op(const spiral_tensor* t) {
     case SPIRAL_OP_GET_ROWS: {
       const spiral_tensor* a = t->src[0];
       const spiral_tensor* ids = t->src[1];
-      if (a == nullptr || ids == nullptr || !is_quant(a) || !quant_layout_ok(a) || !in_spiral_buffer(a)) return 0;
+      if (a == nullptr || ids == nullptr || !is_quant(a) || !planar_whole(a) || !in_spiral_buffer(a)) return 0;
       if (ids->type != SPIRAL_TYPE_I32 || !rows_contiguous(ids, 4) || ids->ne[3] != 1) return 0;
       if (ids->ne[1] != a->ne[2] || ids->ne[2] != a->ne[3]) return 0;
       if (!act_type(t->type) || !rows_contiguous(t, elem_size(t->type))) return 0;
@@ -546,7 +566,7 @@ int spiral_supports_op(const spiral_tensor* t) {
       const spiral_tensor* b = t->src[1];
       const spiral_tensor* ids = t->src[2];
       if (a == nullptr || b == nullptr || ids == nullptr) return 0;
-      if (!is_quant(a) || !quant_layout_ok(a) || !in_spiral_buffer(a) || a->ne[3] != 1) return 0;
+      if (!is_quant(a) || !planar_whole(a) || !in_spiral_buffer(a) || a->ne[3] != 1) return 0;
       if (!act_type(b->type) || !rows_contiguous(b, elem_size(b->type)) || b->ne[3] != 1) return 0;
       if (ids->type != SPIRAL_TYPE_I32 || !fully_contiguous(ids, 4) || ids->ne[2] != 1 || ids->ne[3] != 1) return 0;
       if (t->type != SPIRAL_TYPE_F32 || !fully_contiguous(t, 4)) return 0;

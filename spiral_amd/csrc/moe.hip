@@ -1280,6 +1280,9 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
 
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_expert + 1 + n_pairs); }
 
+// Whether the fused GLU form (streaming kernel only) takes rows of k elements.
+bool moe_glu_fits_k(int64_t k) { return stream_lds_bytes(k) > 0; }
+
 // Arguments validated by the caller. glu_op < 0: plain MUL_MAT_ID; otherwise
 // the fused GLU form (n_rows even), which only the streaming form implements
 // (k <= kStreamMaxK, else SPIRAL_ERR_SHAPE).

@@ -15,14 +15,38 @@
 //        repack.h:46-108).
 // Errors: 0 for a bad shape, short destination, short source stride or a
 // null pointer (src/quants/q4_0/repack.h:33-41). A subnormal fp16 scale is
-// stored as +0; one warning line per call (src/quants/common/repack.h:38-61).
+// stored as +0; one warning line per call (src/quants/common/repack.h:38-61),
+// to stderr or to the callback set with quants_set_repack_warn (the
+// reference routes it with its QUANTS_REPACK_WARN macro,
+// src/quants/common/repack.h:9-14).
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "spiral_quants.h"
 
 namespace {
+
+// Where the warning line goes (quants_set_repack_warn); NULL: stderr.
+std::mutex g_warn_mutex;
+quants_warn_fn g_warn_fn = nullptr;
+void* g_warn_user = nullptr;
+
+void emit_warning(const char* line) {
+  quants_warn_fn fn;
+  void* user;
+  {
+    std::lock_guard<std::mutex> lock(g_warn_mutex);
+    fn = g_warn_fn;
+    user = g_warn_user;
+  }
+  if (fn != nullptr)
+    fn(line, user);
+  else
+    fputs(line, stderr);
+}
 
 struct Geometry {
   const char* name;
@@ -45,12 +69,17 @@ struct Flags {
   bool subnormal = false;
   bool min_int8 = false;
   void report(const char* name) const {
+    char line[128];
     if (subnormal && min_int8)
-      fprintf(stderr, "quants: %s repack flushed subnormal fp16 scales to zero and found -128 int8 weights\n", name);
+      snprintf(line, sizeof line, "quants: %s repack flushed subnormal fp16 scales to zero and found -128 int8 weights\n",
+               name);
     else if (subnormal)
-      fprintf(stderr, "quants: %s repack flushed subnormal fp16 scales to zero\n", name);
+      snprintf(line, sizeof line, "quants: %s repack flushed subnormal fp16 scales to zero\n", name);
     else if (min_int8)
-      fprintf(stderr, "quants: %s repack found -128 int8 weights\n", name);
+      snprintf(line, sizeof line, "quants: %s repack found -128 int8 weights\n", name);
+    else
+      return;
+    emit_warning(line);
   }
 };
 
@@ -165,6 +194,12 @@ int64_t quants_q6_k_record_count(int64_t r, int64_t c) { return record_count(kQ6
 int64_t quants_q6_k_packed_bytes(int64_t r, int64_t c) { return record_count(kQ6_K, r, c) * kQ6_K.record_bytes; }
 int64_t quants_q6_k_repack(const uint8_t* src, int64_t stride, uint8_t* dst, int64_t cap, int64_t r, int64_t c) {
   return repack(kQ6_K, fill_q6_k, src, stride, dst, cap, r, c);
+}
+
+void quants_set_repack_warn(quants_warn_fn fn, void* user) {
+  std::lock_guard<std::mutex> lock(g_warn_mutex);
+  g_warn_fn = fn;
+  g_warn_user = user;
 }
 
 }  // extern "C"

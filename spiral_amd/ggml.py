@@ -39,6 +39,8 @@ Tensor._fields_ = [
     ("op_params", ctypes.c_int32 * MAX_OP_PARAMS),
     ("flags", ctypes.c_int32),
     ("src", ctypes.POINTER(Tensor) * MAX_SRC),
+    ("view_src", ctypes.POINTER(Tensor)),
+    ("view_offs", ctypes.c_size_t),
     ("data", ctypes.c_void_p),
     ("name", ctypes.c_char * MAX_NAME),
 ]
@@ -118,6 +120,27 @@ def _node(qtype, ne, op, srcs, name):
     for i, s in enumerate(srcs):
         t.src[i] = ctypes.pointer(s)
     t._keep = list(srcs)  # keep the sources alive as long as the node
+    return t
+
+
+def view(a, ne, nb, offset, name="view"):
+    """ggml_view_4d(a, ne..., nb1..., offset): a VIEW node of type a.type over
+    a's memory; view_src is the tensor that owns the memory (never a view)
+    and view_offs the byte offset into it, as ggml records them."""
+    ne = list(ne) + [1] * (MAX_DIMS - len(ne))
+    t = new_tensor(a.type, ne, name)
+    t.nb[0] = a.nb[0]
+    for i, v in enumerate(nb, start=1):
+        t.nb[i] = v
+    t.op = OP_VIEW
+    t.src[0] = ctypes.pointer(a)
+    base = a.view_src.contents if a.view_src else a
+    t.view_src = ctypes.pointer(base)
+    t.view_offs = (a.view_offs if a.view_src else 0) + offset
+    if a.data:
+        t.data = a.data + offset
+    t.buffer = a.buffer
+    t._keep = [a, base]
     return t
 
 

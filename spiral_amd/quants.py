@@ -1,9 +1,12 @@
-"""Host mirror of the reference's repack harness (src/quants/tests/common.py).
+"""numpy access to the reference-layout host repack in libspiral_quants.so.
 
-Same names and argument meaning as the reference's Python helpers around its
-C shim (quants_record_count / quants_packed_bytes / quants_repack,
-src/quants/tests/common.py:283-341), backed by libspiral_quants.so's
-quants_<fmt>_* entry points instead of a per-format JIT-compiled shim.
+quants_<fmt>_record_count / packed_bytes / repack are the library's C
+counterparts of the reference's per-format repack API
+(src/quants/q4_0/repack.h:10-111, src/quants/q8_0/repack.h:10-91,
+src/quants/q6_k/repack.h:11-115). They validate every argument themselves
+and return 0 on a bad shape, stride, capacity or pointer; this module sizes
+the output array, makes sure the source array covers the strided view the C
+code will read, and turns a 0 into ValueError.
 """
 
 import ctypes
@@ -12,63 +15,52 @@ import numpy as np
 
 from ._lib import lib
 
-FORMAT_NAMES = ("q4_0", "q8_0", "q6_k")
+FORMATS = ("q4_0", "q8_0", "q6_k")
 
-# Layout constants the reference harness parses from its layout headers
-# (src/quants/tests/common.py:109-170), per format.
-CONSTANTS = {
-    "q4_0": dict(kBlockRows=32, kBlockBytes=18, kTileCols=8, kRecordRows=64, kUnpackTileRows=64,
-                 kChunksPerRecord=1, kPackedRecordBytes=288, kRowsMultiple=256),
-    "q8_0": dict(kBlockRows=32, kBlockBytes=34, kTileCols=8, kRecordRows=256, kUnpackTileRows=256,
-                 kChunksPerRecord=1, kPackedRecordBytes=2176, kRowsMultiple=256),
-    "q6_k": dict(kBlockRows=256, kBlockBytes=210, kTileCols=8, kRecordRows=256, kUnpackTileRows=64,
-                 kChunksPerRecord=4, kPackedRecordBytes=1680, kRowsMultiple=256),
-}
+# Record geometry of the reference's NPU layout (src/quants/TODO.md:366-444):
+# k-rows (the reference's weights_rows) per record and bytes per record of
+# 8 columns; a canonical column is k / block blocks of block_bytes bytes.
+RECORD_ROWS = {"q4_0": 64, "q8_0": 256, "q6_k": 256}
+RECORD_BYTES = {"q4_0": 288, "q8_0": 2176, "q6_k": 1680}
+BLOCK = {"q4_0": (32, 18), "q8_0": (32, 34), "q6_k": (256, 210)}
 
 
-def _fn(format_name, what):
-    if format_name not in FORMAT_NAMES:
-        raise ValueError(f"unknown format: {format_name}")
-    return getattr(lib(), f"quants_{format_name}_{what}")
+def _entry(fmt, what):
+    if fmt not in FORMATS:
+        raise ValueError(f"unknown format {fmt!r}; expected one of {FORMATS}")
+    return getattr(lib(), f"quants_{fmt}_{what}")
 
 
-def record_count(format_name, weights_rows, weights_cols):
-    return _fn(format_name, "record_count")(weights_rows, weights_cols)
+def record_count(fmt, weights_rows, weights_cols):
+    return _entry(fmt, "record_count")(weights_rows, weights_cols)
 
 
-def packed_bytes(format_name, weights_rows, weights_cols):
-    return _fn(format_name, "packed_bytes")(weights_rows, weights_cols)
+def packed_bytes(fmt, weights_rows, weights_cols):
+    return _entry(fmt, "packed_bytes")(weights_rows, weights_cols)
 
 
-def resolve_shape(format_name, rows, cols):
-    """Shape check of src/quants/tests/common.py:187-201."""
-    c = CONSTANTS[format_name]
-    if rows <= 0 or cols <= 0:
-        raise ValueError("rows and cols must be positive")
-    if rows % c["kRowsMultiple"] != 0:
-        raise ValueError(f"rows must be a multiple of {c['kRowsMultiple']}")
-    if cols % c["kTileCols"] != 0:
-        raise ValueError(f"cols must be a multiple of {c['kTileCols']}")
-    return rows, cols, c
+def column_bytes(fmt, weights_rows):
+    """Canonical bytes of one column (one ggml row) of weights_rows elements."""
+    elems, nbytes = BLOCK[fmt]
+    return weights_rows // elems * nbytes
 
 
-def repack_host(format_name, raw, weights_rows, weights_cols, stride):
-    """Repack canonical column-major bytes into the reference's records
-    (src/quants/tests/common.py:308-341)."""
-    if weights_rows <= 0 or weights_cols <= 0:
-        raise ValueError("weights_rows and weights_cols must be positive")
-    if stride < 0:
-        raise ValueError("stride must be non-negative")
-    expected = packed_bytes(format_name, weights_rows, weights_cols)
-    if expected <= 0:
-        raise ValueError(f"{format_name}: invalid shape {weights_rows}x{weights_cols}")
-    raw = np.ascontiguousarray(raw, dtype=np.uint8)
-    if raw.size < weights_cols * stride:
-        raise ValueError(f"{format_name}: source buffer is smaller than the strided view")
-    packed = np.zeros(expected, dtype=np.uint8)
-    written = _fn(format_name, "repack")(
-        raw.ctypes.data_as(ctypes.c_void_p), stride, packed.ctypes.data_as(ctypes.c_void_p),
-        expected, weights_rows, weights_cols)
-    if written != expected:
-        raise RuntimeError(f"{format_name}: repack wrote {written} bytes, expected {expected}")
-    return packed
+def repack(fmt, canonical, weights_rows, weights_cols, col_stride=None):
+    """Canonical GGUF columns (column c at byte c * col_stride of `canonical`)
+    -> the reference's record stream as a new uint8 array."""
+    fn = _entry(fmt, "repack")
+    used = column_bytes(fmt, weights_rows)
+    stride = used if col_stride is None else int(col_stride)
+    size = packed_bytes(fmt, weights_rows, weights_cols)
+    if size <= 0:
+        raise ValueError(f"{fmt}: no record layout for {weights_rows} x {weights_cols}")
+    src = np.ascontiguousarray(canonical, dtype=np.uint8).reshape(-1)
+    # the C side reads used bytes at each of weights_cols column starts
+    if stride >= used and src.size < (weights_cols - 1) * stride + used:
+        raise ValueError(f"{fmt}: {src.size} source bytes do not cover {weights_cols} columns at stride {stride}")
+    out = np.zeros(size, dtype=np.uint8)
+    written = fn(src.ctypes.data_as(ctypes.c_void_p), stride, out.ctypes.data_as(ctypes.c_void_p), size,
+                 weights_rows, weights_cols)
+    if written != size:
+        raise ValueError(f"quants_{fmt}_repack refused the arguments (returned {written})")
+    return out

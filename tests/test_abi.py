@@ -51,7 +51,7 @@ def test_host_repack_matches_reference_fixture(spiral_lib, qtype):
     name = NAMES[qtype]
     raw = fx[f"{name}_raw"]
     rows, cols = (int(v) for v in fx[f"{name}_shape"])
-    got = quants.repack_host(name, raw, rows, cols, O.row_bytes(qtype, rows))
+    got = quants.repack(name, raw, rows, cols, O.row_bytes(qtype, rows))
     assert np.array_equal(got, fx[f"{name}_records"])
 
 
@@ -71,7 +71,7 @@ def test_host_repack_matches_reference_build(spiral_lib, qtype, capfd):
     want = np.zeros(shim.quants_packed_bytes(rows, cols), dtype=np.uint8)
     assert shim.quants_repack(raw.ctypes.data, stride, want.ctypes.data, want.size, rows, cols) == want.size
     ref_err = capfd.readouterr().err
-    got = quants.repack_host(name, raw, rows, cols, stride)
+    got = quants.repack(name, raw, rows, cols, stride)
     ours_err = capfd.readouterr().err
     assert np.array_equal(got, want)
     assert ours_err == ref_err and ours_err.count("\n") == 1
@@ -83,10 +83,10 @@ def test_host_repack_errors_return_zero(spiral_lib, name):
     rc = getattr(L, f"quants_{name}_record_count")
     pb = getattr(L, f"quants_{name}_packed_bytes")
     rp = getattr(L, f"quants_{name}_repack")
-    record_rows = quants.CONSTANTS[name]["kRecordRows"]
+    record_rows = quants.RECORD_ROWS[name]
     assert rc(record_rows, 8) == 1 and rc(record_rows, 7) == 0 and rc(record_rows - 32, 8) == 0
     assert rc(0, 8) == 0 and rc(record_rows, 0) == 0 and rc(-record_rows, 8) == 0
-    assert pb(record_rows * 2, 16) == 4 * quants.CONSTANTS[name]["kPackedRecordBytes"]
+    assert pb(record_rows * 2, 16) == 4 * quants.RECORD_BYTES[name]
     qtype = {"q4_0": O.Q4_0, "q8_0": O.Q8_0, "q6_k": O.Q6_K}[name]
     stride = O.row_bytes(qtype, record_rows)
     src = np.zeros(8 * stride, dtype=np.uint8)
@@ -163,3 +163,63 @@ def test_validation_before_device_work(spiral_lib):
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, p, 8192, None) == 4
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 8, p, _lib.TYPE_F32, 4, None, 0, None) == 4
         assert L.quants_unpack_all(q4, p, 64, 8, p, None) == 4
+
+
+def test_repack_warning_route(spiral_lib, capfd):
+    """quants_set_repack_warn reroutes the one warning line of a repack (the
+    reference's QUANTS_REPACK_WARN, src/quants/common/repack.h:9-14): to the
+    callback while one is set, to nothing with a callback that drops it, and
+    back to stderr after resetting to NULL."""
+    rows, cols = 64, 8
+    raw = synth_q4_0_columns(rows, cols)
+    raw.reshape(cols, -1, 18)[3, 1, :2] = (0x01, 0x00)  # one subnormal scale
+    lines = []
+    cb_type = ctypes.CFUNCTYPE(None, ctypes.c_char_p, ctypes.c_void_p)
+    keep = cb_type(lambda line, user: lines.append((line.decode(), user)))
+    drop = cb_type(lambda line, user: None)
+    L = spiral_lib
+    try:
+        L.quants_set_repack_warn(ctypes.cast(keep, ctypes.c_void_p), ctypes.c_void_p(1234))
+        quants.repack("q4_0", raw, rows, cols)
+        assert lines == [("quants: Q4_0 repack flushed subnormal fp16 scales to zero\n", 1234)]
+        assert capfd.readouterr().err == ""
+        L.quants_set_repack_warn(ctypes.cast(drop, ctypes.c_void_p), None)
+        quants.repack("q4_0", raw, rows, cols)
+        assert capfd.readouterr().err == "" and len(lines) == 1
+    finally:
+        L.quants_set_repack_warn(None, None)
+    quants.repack("q4_0", raw, rows, cols)
+    assert capfd.readouterr().err == "quants: Q4_0 repack flushed subnormal fp16 scales to zero\n"
+
+
+def synth_q4_0_columns(rows, cols):
+    from spiral_amd import synth
+    return synth.make_weights(O.Q4_0, cols, rows, 3)
+
+
+def test_repack_wrapper_checks_the_source_span(spiral_lib):
+    """The numpy wrapper refuses a source array shorter than the strided view
+    the C entry point reads, and reports the entry point's 0 as an error."""
+    rows, cols = 64, 8
+    raw = synth_q4_0_columns(rows, cols)
+    with pytest.raises(ValueError, match="do not cover"):
+        quants.repack("q4_0", raw[:-1], rows, cols)
+    with pytest.raises(ValueError, match="do not cover"):
+        quants.repack("q4_0", raw, rows, cols, col_stride=O.row_bytes(O.Q4_0, rows) + 1)
+    with pytest.raises(ValueError, match="refused"):
+        quants.repack("q4_0", raw, rows, cols, col_stride=O.row_bytes(O.Q4_0, rows) - 1)
+    with pytest.raises(ValueError, match="no record layout"):
+        quants.repack("q4_0", raw, rows - 32, cols)
+    assert quants.repack("q4_0", raw, rows, cols).size == quants.RECORD_BYTES["q4_0"]
+
+
+def test_glu_fits_predicate(spiral_lib):
+    L = spiral_lib
+    q4, q6 = _lib.TYPE_Q4_0, _lib.TYPE_Q6_K
+    assert L.spiral_mul_mat_id_glu_fits(q4, 1536, 2048) == 1
+    assert L.spiral_mul_mat_id_glu_fits(q4, 1536, 4096) == 1
+    assert L.spiral_mul_mat_id_glu_fits(q4, 1536, 4096 + 32) == 0
+    assert L.spiral_mul_mat_id_glu_fits(q4, 1535, 2048) == 0
+    assert L.spiral_mul_mat_id_glu_fits(q6, 64, 2048) == 1
+    assert L.spiral_mul_mat_id_glu_fits(q6, 64, 2048 + 32) == 0
+    assert L.spiral_mul_mat_id_glu_fits(_lib.TYPE_F32, 64, 2048) == 0

@@ -171,6 +171,53 @@ def test_stacks_must_be_16_byte_matrices(cuda):
 
 
 @pytest.mark.gpu
+def test_quantized_views(cuda):
+    """Views into quantized weights (ggml_view_*: view_src / view_offs). The
+    planar layout is relative to each matrix's start, so a view inside a
+    matrix (a row range, or a matrix-sized window at a partial offset) is
+    refused by supports_op, set_tensor, get_tensor and memset_tensor, even
+    though its own strides and alignment look like a whole tensor's. A view
+    of one whole matrix of a stack is accepted: MUL_MAT over it is that
+    matrix's product and get_tensor returns its canonical bytes."""
+    qtype, k, n, n_mat, m = O.Q4_0, 256, 64, 3, 2
+    raws = [synth.make_weights(qtype, n, k, 80 + i) for i in range(n_mat)]
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, n, n_mat]))
+    buf.set(a, np.concatenate(raws).tobytes())
+    rb, mat = a.nb[1], a.nb[2]
+    xf = np.random.default_rng(5).standard_normal((m, k), dtype=np.float32)
+    b = buf.alloc(ggml.new_tensor(ggml.TYPE_F32, [k, m]))
+    buf.set(b, xf.tobytes())
+    L = ggml._lib()
+    bad_views = [ggml.view(a, [k, 32], [rb], 16 * rb),     # rows 16..47 of matrix 0
+                 ggml.view(a, [k, n], [rb], 16 * rb),      # a matrix-sized window at a partial offset
+                 ggml.view(a, [k, 32], [rb], mat)]         # the first half of matrix 1
+    for v in bad_views:
+        assert v.data % 16 == 0 and v.buffer
+        assert not ggml.supports_op(ggml.mul_mat(v, b))
+        assert not ggml.supports_op(ggml.get_rows(v, ggml.new_tensor(ggml.TYPE_I32, [2])))
+        host = (ctypes.c_uint8 * rb)()
+        for fn in (L.spiral_buffer_set_tensor, L.spiral_buffer_get_tensor):
+            assert STATUS[fn(buf.ptr, ctypes.byref(v), host, 0, rb)] == "SPIRAL_ERR_SHAPE"
+        assert STATUS[L.spiral_buffer_memset_tensor(buf.ptr, ctypes.byref(v), 0, 0, rb)] == "SPIRAL_ERR_SHAPE"
+    one = ggml.view(a, [k, n], [rb], mat)  # matrix 1, whole
+    nested = ggml.view(ggml.view(a, [k, n, 2], [rb, mat], mat), [k, n], [rb], mat)  # matrix 2 via a view of a view
+    assert nested.view_offs == 2 * mat and ctypes.addressof(nested.view_src.contents) == ctypes.addressof(a)
+    be = ggml.Backend(0)
+    for v, i in ((one, 1), (nested, 2)):
+        node = buf.alloc(ggml.mul_mat(v, b))
+        assert ggml.supports_op(node)
+        assert be.graph_compute([node]) == 0
+        be.synchronize()
+        y = np.frombuffer(buf.get(node), dtype=np.float32).reshape(m, n)
+        ref = O.matmul_f64(O.dequant(qtype, raws[i], n, k), synth.bf16_bits(xf))
+        assert rel_err(y, ref) <= REL_TOL_EXACT_W
+        assert buf.get(v) == raws[i].tobytes()
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
 @pytest.mark.parametrize("act", [ggml.TYPE_F32, ggml.TYPE_BF16])
 @pytest.mark.parametrize("m", [1, 6, 40])
@@ -295,6 +342,29 @@ def test_mul_mat_id_then_glu_fused_and_not(cuda):
         for s in range(top_k):
             p_ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], 2 * F, k), xb[t][None])[0]
             assert rel_err(p[t, s], p_ref) <= REL_TOL_EXACT_W
+    # A GLU output with padded rows (row stride F + 8 floats): the fused pass
+    # writes packed rows, so graph_compute must run the two nodes unfused and
+    # GLU honours the stride; the pad floats are never written.
+    prod.flags = 0
+    pad = 8
+    gp = ggml.glu(prod, ggml.GLU_SWIGLU)
+    gp.nb[1] = (F + pad) * 4
+    gp.nb[2] = gp.nb[1] * top_k
+    gp.nb[3] = gp.nb[2] * n_tokens
+    gp_bytes = ggml.nbytes(gp)  # ggml_nbytes: the last row's pad is not part of the tensor
+    assert gp_bytes == gp.nb[3] - pad * 4
+    gp = buf.alloc(gp)
+    assert ggml.supports_op(gp)
+    L = ggml._lib()
+    fill = (ctypes.c_uint8 * gp_bytes).from_buffer_copy(np.full(gp_bytes // 4, 5.0, np.float32).tobytes())
+    assert L.spiral_buffer_set_tensor(buf.ptr, ctypes.byref(gp), fill, 0, gp_bytes) == 0
+    assert be.graph_compute([prod, gp]) == 0
+    be.synchronize()
+    out = (ctypes.c_uint8 * gp.nb[3]).from_buffer_copy(np.full(gp.nb[3] // 4, 5.0, np.float32).tobytes())
+    assert L.spiral_buffer_get_tensor(buf.ptr, ctypes.byref(gp), out, 0, gp_bytes) == 0
+    rows = np.frombuffer(bytes(out), dtype=np.float32).reshape(n_tokens, top_k, F + pad)
+    assert rows[:, :, :F].tobytes() == y.tobytes()
+    assert (rows[:, :, F:] == 5.0).all()
     be.free()
     buf.free()
 

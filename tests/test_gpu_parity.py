@@ -373,6 +373,20 @@ def test_moe_128_experts_gate_up(cuda):
     assert err <= REL_TOL
 
 
+def test_moe_128_experts_down(cuda):
+    """The MoE workload's down stage at its own size: 128 experts of 2048 x
+    768 Q4_0, per-slot inputs [64][8][768] (x_slots = top_k = 8), 64 tokens,
+    top-8 distinct experts per token; every one of the 512 (token, slot)
+    rows against the float64 oracle (src/quants/tests/mmul.py:104-126)."""
+    y, ref, ids = _moe_case(cuda, O.Q4_0, 128, 2048, 768, 64, 8, 8, 16, torch.bfloat16)
+    assert np.unique(ids).size > 100
+    err = rel_err(y, ref)
+    print(f"moe down: rel err {err:.2e}")
+    assert err <= REL_TOL
+    y32, ref32, _ = _moe_case(cuda, O.Q4_0, 128, 2048, 768, 64, 8, 8, 16, torch.float32)
+    assert rel_err(y32, ref32) <= REL_TOL_EXACT_W
+
+
 @pytest.mark.parametrize("n,k_blocks,x_slots", [(72, 9, 1), (200, 24, 3), (8, 1, 1), (130, 72, 1)])
 def test_moe_edges(cuda, n, k_blocks, x_slots):
     """Q4_0 MoE over its edges: k not a multiple of 128 (a short last step),
@@ -425,7 +439,7 @@ def test_ref_unpack_mmul_all(cuda, qtype):
     rows, cols = 512, 48
     raw = synth.make_weights(qtype, cols, rows, 40)
     from spiral_amd import quants
-    rec = quants.repack_host(NAMES[qtype], raw, rows, cols, O.row_bytes(qtype, rows))
+    rec = quants.repack(NAMES[qtype], raw, rows, cols, O.row_bytes(qtype, rows))
     rng = np.random.default_rng(41)
     inputs_rows = rng.integers(-4, 5, (4, rows)).astype(np.float32)  # src/quants/tests/mmul.py:22-35
     tiled = inputs_rows.reshape(4, rows // 8, 8).transpose(1, 0, 2).reshape(-1)

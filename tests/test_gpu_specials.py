@@ -1,0 +1,201 @@
+"""Edge-case weights through every product kernel, on the GPU, through the C ABI.
+
+Each product kernel decodes the packed blocks on its own path (the GEMV's
+offset codes, the GEMM / small-batch pieces, the MoE stream pieces), so the
+special cases the dequant tests pin must also pass through each of them:
+
+  - block scales with exponent 0 (+0, -0, subnormals): the reference's
+    device decode gives +0 (src/quants/common/scale.aie.h:24-26) -- rows
+    whose every scale is such give exactly 0;
+  - exponent 31: the finite value sign * 2^16 * (1 + m/1024)
+    (src/quants/common/scale.aie.h:19-23), not inf / NaN;
+  - Q8_0 code -128, which the reference accepts with a warning
+    (src/quants/q8_0/repack.h:73-83);
+  - Q6_K sub-scales over the whole int8 range, negative ones and -128
+    included (src/quants/q6_k/unpack.aie.h:33-61).
+
+Bar: rows whose scales all decode to zero are exactly 0. Every other output
+is held to |y - ref| <= TOL * sum_k |w[n][k] x[m][k]|, with ref the float64
+product over the oracle's exact bf16 weights (src/quants/tests/mmul.py:104-112):
+the sum of absolute terms is the scale of an fp32 dot product's rounding
+error and, unlike |ref|, does not collapse under cancellation or let the
+2^16-scaled rows hide the others. A lost or mis-decoded block moves a row by
+a sizeable fraction of that sum (about 1/sqrt(32) of it for one random block).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from spiral_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [O.Q4_0, O.Q8_0, O.Q6_K]
+TOL_BF16_OUT = 1e-2     # bf16 outputs (one rounding of the result)
+TOL_F32_OUT = 1e-3      # float32 outputs of the exact-weight MFMA paths
+TOL_F32_GEMV = 5e-3     # float32 GEMV output: codes unrounded, scale after the block sum
+
+# fp16 scale patterns with exponent 0 (decode to +0) and exponent 31 / the
+# normal extremes (decode to finite values).
+ZERO_SCALES = np.array([0x0000, 0x8000, 0x0001, 0x03FF, 0x83FF, 0x8001], dtype=np.uint16)
+BIG_SCALES = np.array([0x7C00, 0xFC01, 0x7FFF, 0xFFFF, 0x7BFF, 0xFBFF, 0x0400, 0x8400], dtype=np.uint16)
+N_ZERO_ROWS = 3
+
+
+def dev_u8(a, device):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).to(device)
+
+
+def dev_bf16(a_u16, device):
+    return torch.from_numpy(np.ascontiguousarray(a_u16, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def special_weights(qtype, n_rows, k, seed):
+    """Canonical blocks with the edge cases above. Rows 0..N_ZERO_ROWS-1 have
+    only exponent-0 scales; the other rows get exponent-31 and extreme normal
+    scales on random blocks, Q8_0 codes of -128 and (Q6_K) random int8
+    sub-scales over the whole range."""
+    raw = synth.make_weights(qtype, n_rows, k, seed)
+    bb = O.BLOCK_BYTES[qtype]
+    nb = k // O.BLOCK_ELEMS[qtype]
+    blocks = raw.reshape(n_rows, nb, bb)
+    rng = np.random.default_rng(seed + 17)
+    dpos = 208 if qtype == O.Q6_K else 0
+
+    def set_d(r, b, h):
+        blocks[r, b, dpos] = h & 0xFF
+        blocks[r, b, dpos + 1] = h >> 8
+
+    for r in range(min(N_ZERO_ROWS, n_rows)):
+        for b in range(nb):
+            set_d(r, b, int(ZERO_SCALES[(r * nb + b) % ZERO_SCALES.size]))
+    for r in range(N_ZERO_ROWS, n_rows):
+        for b in rng.choice(nb, min(nb, 2), replace=False):
+            set_d(r, b, int(rng.choice(BIG_SCALES)))
+        if rng.random() < 0.3:  # an exponent-0 block inside an ordinary row
+            set_d(r, int(rng.integers(nb)), int(rng.choice(ZERO_SCALES)))
+    if qtype == O.Q8_0:
+        qs = blocks[:, :, 2:]
+        qs[rng.random(qs.shape) < 0.1] = 0x80  # code -128
+    if qtype == O.Q6_K:
+        sc = blocks[:, :, 192:208]
+        pick = rng.random(sc.shape) < 0.5
+        sc[pick] = rng.integers(0, 256, int(pick.sum()), dtype=np.uint8)
+        sc[:, 0, 0] = 0x80  # -128 in every row
+    return raw
+
+
+def abs_bits(u16):
+    return np.asarray(u16, dtype=np.uint16) & np.uint16(0x7FFF)
+
+
+def check_product(y, w_bits, x_bits, tol, zero_rows=N_ZERO_ROWS):
+    """y [m, n] against the float64 oracle over bf16 weights w_bits [n, k]."""
+    y = np.asarray(y, dtype=np.float64)
+    ref = O.matmul_f64(w_bits, x_bits)
+    scale = O.matmul_f64(abs_bits(w_bits), abs_bits(x_bits))
+    assert np.isfinite(y).all()
+    assert (y[:, :zero_rows] == 0).all(), "rows whose scales all decode to +0 must be exactly 0"
+    assert (scale[:, zero_rows:] > 0).all()
+    err = np.abs(y[:, zero_rows:] - ref[:, zero_rows:]) / scale[:, zero_rows:]
+    assert err.max() <= tol, float(err.max())
+    return float(err.max())
+
+
+def run_mul_mat(cuda, qtype, n, k, m, seed, out_dtype):
+    raw = special_weights(qtype, n, k, seed)
+    x = synth.make_x(m, k, seed + 1)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    y = ops.mul_mat(qtype, w, n, k, dev_bf16(x, cuda), out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy(), O.dequant(qtype, raw, n, k), x
+
+
+# k: one pass with x in registers, and several passes with x read from LDS
+GEMV_K = {O.Q4_0: (32 * 12, 32 * 288), O.Q8_0: (32 * 12, 32 * 160), O.Q6_K: (256 * 3, 256 * 24)}
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gemv_special_weights(cuda, qtype, out_dtype):
+    for k in GEMV_K[qtype]:
+        y, wb, x = run_mul_mat(cuda, qtype, 67, k, 1, 100 + k, out_dtype)
+        tol = TOL_BF16_OUT if out_dtype == torch.bfloat16 else TOL_F32_GEMV
+        check_product(y, wb, x, tol)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("m", [2, 4, 16])
+def test_small_batch_special_weights(cuda, qtype, m):
+    k = O.BLOCK_ELEMS[qtype] * (13 if qtype != O.Q6_K else 5)
+    y, wb, x = run_mul_mat(cuda, qtype, 70, k, m, 200 + m, torch.float32)
+    check_product(y, wb, x, TOL_F32_OUT)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_small_batch_windows_special_weights(cuda, qtype):
+    """k wide enough that 16 rows of x are staged in windows."""
+    k = 8192 if qtype != O.Q6_K else 14336
+    y, wb, x = run_mul_mat(cuda, qtype, 40, k, 16, 300, torch.float32)
+    check_product(y, wb, x, TOL_F32_OUT)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("m", [17, 130])
+def test_gemm_special_weights(cuda, qtype, m):
+    k = O.BLOCK_ELEMS[qtype] * (9 if qtype != O.Q6_K else 3)
+    for out_dtype, tol in ((torch.float32, TOL_F32_OUT), (torch.bfloat16, TOL_BF16_OUT)):
+        y, wb, x = run_mul_mat(cuda, qtype, 150, k, m, 400 + m, out_dtype)
+        check_product(y, wb, x, tol)
+
+
+def moe_special_case(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed):
+    rng = np.random.default_rng(seed)
+    per = O.row_bytes(qtype, k) * n
+    raws = [special_weights(qtype, n, k, seed * 100 + e) for e in range(n_expert)]
+    w = torch.empty(n_expert * per, dtype=torch.uint8, device=cuda)
+    for e, r in enumerate(raws):
+        w[e * per:(e + 1) * per] = ops.to_planar(qtype, dev_u8(r, cuda), n, k)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    x = synth.make_x(n_tokens * x_slots, k, seed + 3).reshape(n_tokens, x_slots, k)
+    deq = [O.dequant(qtype, r, n, k) for r in raws]
+    return w, per, ids, x, deq
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("k_mult", [1, 24])
+def test_mul_mat_id_special_weights(cuda, qtype, k_mult):
+    """Both MoE kernels: the streaming form (k <= 4096) and the tiled form
+    (k_mult = 24: k above 4096 for every format)."""
+    k = O.BLOCK_ELEMS[qtype] * (4 if qtype != O.Q6_K else 1) * k_mult
+    if qtype == O.Q6_K and k_mult > 1:
+        k = 256 * 20
+    n_expert, n, n_tokens, top_k, x_slots = 6, 48, 20, 3, 3
+    w, per, ids, x, deq = moe_special_case(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, 50 + k_mult)
+    y = ops.mul_mat_id(qtype, w, per, n_expert, n, k, dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda),
+                       out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    for t in range(n_tokens):
+        for s in range(top_k):
+            check_product(y[t, s][None, :], deq[ids[t, s]], x[t, s % x_slots][None, :], TOL_F32_OUT)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_mul_mat_id_glu_special_weights(cuda, qtype):
+    """Fused MUL_MAT_ID + SwiGLU over edge-case gate/up experts: equal to the
+    unfused chain bit for bit, and the product inside it on the oracle's bar."""
+    k = O.BLOCK_ELEMS[qtype] * (8 if qtype != O.Q6_K else 2)
+    n_expert, F, n_tokens, top_k = 5, 40, 18, 2
+    w, per, ids, x, deq = moe_special_case(cuda, qtype, n_expert, 2 * F, k, n_tokens, top_k, 1, 77)
+    xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
+    prod = ops.mul_mat_id(qtype, w, per, n_expert, 2 * F, k, xd, idd, out_dtype=torch.float32)
+    fused = ops.mul_mat_id_glu(qtype, w, per, n_expert, 2 * F, k, xd, idd, ops.GLU_SWIGLU, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ops.glu(prod, ops.GLU_SWIGLU))
+    p = prod.cpu().numpy()
+    for t in range(n_tokens):
+        for s in range(top_k):
+            check_product(p[t, s][None, :], deq[ids[t, s]], x[t, 0][None, :], TOL_F32_OUT)
