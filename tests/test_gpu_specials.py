@@ -97,9 +97,13 @@ def check_product(y, w_bits, x_bits, tol, zero_rows=N_ZERO_ROWS):
     ref = O.matmul_f64(w_bits, x_bits)
     scale = O.matmul_f64(abs_bits(w_bits), abs_bits(x_bits))
     assert np.isfinite(y).all()
-    assert (y[:, :zero_rows] == 0).all(), "rows whose scales all decode to +0 must be exactly 0"
-    assert (scale[:, zero_rows:] > 0).all()
-    err = np.abs(y[:, zero_rows:] - ref[:, zero_rows:]) / scale[:, zero_rows:]
+    # every weight of these outputs is zero (the designated rows, and rows
+    # whose only blocks drew an exponent-0 scale): exactly 0
+    zero = scale == 0
+    assert zero[:, :zero_rows].all()
+    assert (y[zero] == 0).all(), "outputs whose weights all decode to +0 must be exactly 0"
+    assert (~zero).sum() > zero.shape[0]
+    err = np.abs(y[~zero] - ref[~zero]) / scale[~zero]
     assert err.max() <= tol, float(err.max())
     return float(err.max())
 
