@@ -195,6 +195,26 @@ int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride,
                       int64_t n_tokens, int64_t top_k, void* y, int y_type,
                       void* workspace, int64_t workspace_bytes, void* stream);
 
+/* spiral_mul_mat_id for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops or harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Arguments, results and errors as
+ * spiral_mul_mat_id, without the workspace: the routing lists live in a
+ * library-owned device array of SPIRAL_MUL_MAT_ID_STATIC_BYTES per GPU, held
+ * until the process ends. A shape whose lists need more
+ * (spiral_mul_mat_id_workspace_bytes(n_expert, n_tokens, top_k) above that:
+ * about 262,000 experts plus (token, slot) pairs) fails with
+ * SPIRAL_ERR_CAPACITY before anything runs. Calls no hipMalloc / hipFree.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (on different streams, or from different host threads) race;
+ * calls ordered on one stream do not. */
+#define SPIRAL_MUL_MAT_ID_STATIC_BYTES (1 << 20)
+int spiral_mul_mat_id_noalloc(int type, const void* w, int64_t expert_stride,
+                              int64_t n_expert, int64_t n_rows, int64_t k,
+                              const uint16_t* x, int64_t x_slots,
+                              const int32_t* ids, int64_t n_tokens,
+                              int64_t top_k, void* y, int y_type,
+                              void* stream);
+
 /* ggml GLU variants, numbered as ggml's ggml_glu_op: out = act(a) * b over
  * the two halves (a, b) of a row of 2F values, a the first half unless
  * swapped. act: REGLU relu, GEGLU gelu (tanh form), SWIGLU silu, GEGLU_ERF

@@ -53,6 +53,8 @@ SIGNATURES = {
     "spiral_mul_mat_id_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "spiral_mul_mat_id": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,
                                  _p, _i64, _p]),
+    "spiral_mul_mat_id_noalloc": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,
+                                         _p]),
     "spiral_mul_mat_id_glu_fits": (_int, [_int, _i64, _i64]),
     "spiral_mul_mat_id_glu": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _int, _int,
                                      _p, _int, _p, _i64, _p]),

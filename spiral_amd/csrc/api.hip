@@ -18,6 +18,7 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
 int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
         hipStream_t s);
 bool moe_glu_fits_k(int64_t k);
+void* moe_static_scratch(int& rc);
 
 bool glu_op_ok(int op) {
   return op == SPIRAL_GLU_REGLU || op == SPIRAL_GLU_GEGLU || op == SPIRAL_GLU_SWIGLU ||
@@ -100,6 +101,25 @@ int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_
   if (rc != SPIRAL_OK) return rc;
   return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, -1, 0,
              workspace, static_cast<hipStream_t>(stream));
+}
+
+int spiral_mul_mat_id_noalloc(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,
+                              int64_t k, const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens,
+                              int64_t top_k, void* y, int y_type, void* stream) {
+  if (n_tokens == 0 && is_quant_type(type) && (y_type == SPIRAL_TYPE_BF16 || y_type == SPIRAL_TYPE_F32))
+    return SPIRAL_OK;
+  // Validated as spiral_mul_mat_id with a stand-in workspace of the static
+  // array's size (never dereferenced here); the real address comes after.
+  static uint32_t probe_ws[4];
+  int rc = check_mul_mat_id(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type,
+                            probe_ws, SPIRAL_MUL_MAT_ID_STATIC_BYTES);
+  if (rc != SPIRAL_OK) return rc;
+  rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  void* ws = moe_static_scratch(rc);
+  if (rc != SPIRAL_OK) return rc;
+  return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, -1, 0, ws,
+             static_cast<hipStream_t>(stream));
 }
 
 int spiral_mul_mat_id_glu_fits(int type, int64_t n_rows, int64_t k) {

@@ -47,6 +47,7 @@
 // act(gate) * up (act(up) * gate when swapped) to a [pair][F] output, so
 // the [pair][2F] product never reaches memory.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 #include "dequant_impl.h"
@@ -1282,6 +1283,42 @@ int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_e
 
 // Whether the fused GLU form (streaming kernel only) takes rows of k elements.
 bool moe_glu_fits_k(int64_t k) { return stream_lds_bytes(k) > 0; }
+
+// ---- library-owned routing scratch (spiral_mul_mat_id_noalloc) -------------
+//
+// One array per GPU, in the code object's device memory, for callers that
+// cannot allocate: the routing lists of a MUL_MAT_ID (offsets and list, see
+// route_kernel) go here instead of a caller workspace. route_kernel writes
+// every entry it later reads, so nothing needs clearing between calls. In
+// host code `scratch` only names the symbol; its device address comes from
+// hipGetSymbolAddress, once per device (each GPU has its own copy).
+static __device__ __align__(256) uint8_t scratch[SPIRAL_MUL_MAT_ID_STATIC_BYTES];
+
+// Device address of the current device's scratch (looked up once per device
+// under a lock), or nullptr with rc set.
+void* moe_static_scratch(int& rc) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    rc = SPIRAL_ERR_HIP;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      rc = SPIRAL_ERR_HIP;
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  rc = SPIRAL_OK;
+  return addr[dev];
+}
 
 // Arguments validated by the caller. glu_op < 0: plain MUL_MAT_ID; otherwise
 // the fused GLU form (n_rows even), which only the streaming form implements
