@@ -1,8 +1,9 @@
 /*
  * spiral_quants.h -- C ABI of libspiral_quants.so, the MI355X (gfx950)
  * implementation of spiral's quantized-weight hot path: GGUF Q4_0 / Q8_0 /
- * Q6_K block dequantization to bf16 and the dequant-fused matrix products
- * behind a ggml backend's MUL_MAT / GET_ROWS / MUL_MAT_ID.
+ * Q6_K (and the K-quants Q4_K / Q5_K the reference plans) block
+ * dequantization to bf16 and the dequant-fused matrix products behind a ggml
+ * backend's MUL_MAT / GET_ROWS / MUL_MAT_ID.
  *
  * Conventions
  *  - Plain C types only. Device pointers are HIP device memory; `stream` is a
@@ -46,6 +47,8 @@ enum {
   SPIRAL_TYPE_F16 = 1,
   SPIRAL_TYPE_Q4_0 = 2,
   SPIRAL_TYPE_Q8_0 = 8,
+  SPIRAL_TYPE_Q4_K = 12,
+  SPIRAL_TYPE_Q5_K = 13,
   SPIRAL_TYPE_Q6_K = 14,
   SPIRAL_TYPE_I32 = 26,
   SPIRAL_TYPE_BF16 = 30
@@ -127,6 +130,10 @@ int quants_unpack_mmul_all(int type, const void* packed,
  *   Q4_0: qs[n_rows][k/32][16]  | d[n_rows][k/32] (fp16)                     *
  *   Q8_0: qs[n_rows][k/32][32]  | d[n_rows][k/32]                            *
  *   Q6_K: ql[n_rows][k/256][128] | qh[..][64] | sc[..][16] | d[n_rows][k/256] *
+ *   Q4_K: qs[n_rows][k/256][128] | meta[..][16]                              *
+ *   Q5_K: qs[n_rows][k/256][128] | qh[..][32] | meta[..][16]                 *
+ * (meta: a K-quant block's first 16 canonical bytes, fp16 d, fp16 dmin and  *
+ * the 12 packed 6-bit scale/min bytes, kept together for one 16-byte load). *
  * This is the GPU counterpart of the reference's load-time repack           *
  * (src/quants/TODO.md:303-334). Weight pointers below are planar and must be *
  * 16-byte aligned.                                                          *
@@ -148,7 +155,10 @@ int spiral_from_planar(int type, const void* src, int64_t n_rows, int64_t k,
  * values are bf16_rne(code * d) (Q4_0 code q-8, Q8_0 int8) and
  * bf16_rne(d * sc * (q-32)) (Q6_K), d decoded as the reference's device does
  * (exponent 0 -> +0; src/quants/common/scale.aie.h:9-27). Bit-identical to
- * the reference's unpack (src/quants/<fmt>/unpack.aie.h). */
+ * the reference's unpack (src/quants/<fmt>/unpack.aie.h).
+ * Q4_K / Q5_K (planned by the reference, src/quants/TODO.md:80-107, with no
+ * code to match): bf16_rne(fma(d * scale, q, -dmin * min)), d and dmin IEEE
+ * binary16 (subnormals keep their value, as in ggml), one float rounding. */
 int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k,
                         uint16_t* out, int64_t ld_out, void* stream);
 

@@ -185,6 +185,8 @@ int oq_block_bytes(int type) {
     case OQ_Q4_0: return 18;  /* src/quants/q4_0/layout.h:11-12 */
     case OQ_Q8_0: return 34;  /* src/quants/q8_0/layout.h:11-12 */
     case OQ_Q6_K: return 210; /* src/quants/q6_k/layout.h:11-12 */
+    case OQ_Q4_K: return 144; /* d, dmin, scales[12], qs[128] */
+    case OQ_Q5_K: return 176; /* d, dmin, scales[12], qh[32], qs[128] */
     default: return 0;
   }
 }
@@ -194,6 +196,8 @@ int oq_block_elems(int type) {
     case OQ_Q4_0: return 32;
     case OQ_Q8_0: return 32;
     case OQ_Q6_K: return 256;
+    case OQ_Q4_K: return 256;
+    case OQ_Q5_K: return 256;
     default: return 0;
   }
 }
@@ -201,8 +205,12 @@ int oq_block_elems(int type) {
 /* Exact values of one block's weights. Every product below is exact in
  * float (Q4_0 <= 15, Q8_0 <= 19, Q6_K <= 23 significant bits), so rounding
  * these to bf16 is the format's single rounding. */
+static void kq_dequant(int type, const uint8_t* blk, float* yf, double* yd);
+
 static void dequant_block_exact(int type, const uint8_t* blk, double* y) {
-  if (type == OQ_Q4_0) {
+  if (type == OQ_Q4_K || type == OQ_Q5_K) {
+    kq_dequant(type, blk, NULL, y);
+  } else if (type == OQ_Q4_0) {
     /* src/quants/tests/formats/q4_0.py:53-60: low nibbles are elements 0..15,
      * high nibbles 16..31, value (q - 8) * d. */
     const float d = oq_fp16_device(le16(blk));
@@ -241,7 +249,81 @@ static void dequant_block_exact(int type, const uint8_t* blk, double* y) {
   }
 }
 
+/* ---- K-quants with 6-bit scales and mins (Q4_K, Q5_K) --------------------
+ *
+ * The reference plans these formats but has no code or vectors for them
+ * (src/quants/TODO.md:16-17,80-107): 256-element super-blocks of eight
+ * 32-element groups, fp16 d and dmin, a 6-bit scale and a 6-bit min per
+ * group packed into 12 bytes, element value d * scale * q - dmin * min, and
+ * Q5_K's extra high bit. The byte layout is ggml's block_q4_K / block_q5_K.
+ *
+ * The 12 scale bytes, field by field:
+ *   bytes 0..3   bits 0..5: scale of groups 0..3; bits 6..7: bits 4..5 of
+ *                the scale of groups 4..7
+ *   bytes 4..7   bits 0..5: min of groups 0..3; bits 6..7: bits 4..5 of the
+ *                min of groups 4..7
+ *   bytes 8..11  bits 0..3: bits 0..3 of the scale of groups 4..7;
+ *                bits 4..7: bits 0..3 of the min of groups 4..7
+ * Group g (elements 32 g .. 32 g + 31) takes the low (g even) or high (g odd)
+ * nibble of qs[32 (g / 2) + l], and for Q5_K bit g of qh[l] as bit 4 of its
+ * code (l < 32).
+ *
+ * d and dmin decode as IEEE binary16 (subnormals keep their value), as
+ * ggml's dequantization does: the reference's exponent-0 flush
+ * (src/quants/common/repack.h:29-34) belongs to its NPU scale loader for the
+ * formats it implements, and a K-quant's dmin is often subnormal in real
+ * files. d * scale and dmin * min are exact in float; the element is
+ * fmaf(d * scale, q, -dmin * min), one rounding to float, then bf16 RNE. */
+static void kq_scale_min(const uint8_t* s, int g, int* sc, int* mn) {
+  if (g < 4) {
+    *sc = s[g] & 63;
+    *mn = s[4 + g] & 63;
+  } else {
+    const int i = g - 4;
+    *sc = (s[8 + i] & 15) | ((s[i] >> 6) << 4);
+    *mn = (s[8 + i] >> 4) | ((s[4 + i] >> 6) << 4);
+  }
+}
+
+/* Codes (0..15 or 0..31) of the 256 elements of a K-quant super-block. */
+static void kq_codes(int type, const uint8_t* blk, int* q) {
+  const uint8_t* qs = blk + (type == OQ_Q5_K ? 48 : 16);
+  const uint8_t* qh = blk + 16;
+  for (int g = 0; g < 8; ++g) {
+    for (int l = 0; l < 32; ++l) {
+      const uint8_t b = qs[32 * (g / 2) + l];
+      int c = (g & 1) ? (b >> 4) : (b & 15);
+      if (type == OQ_Q5_K) c |= ((qh[l] >> g) & 1) << 4;
+      q[32 * g + l] = c;
+    }
+  }
+}
+
+static void kq_dequant(int type, const uint8_t* blk, float* yf, double* yd) {
+  const float d = oq_fp16_ieee(le16(blk)), dmin = oq_fp16_ieee(le16(blk + 2));
+  int q[256];
+  kq_codes(type, blk, q);
+  for (int g = 0; g < 8; ++g) {
+    int sc, mn;
+    kq_scale_min(blk + 4, g, &sc, &mn);
+    const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+    for (int l = 0; l < 32; ++l) {
+      const int e = 32 * g + l;
+      if (yf) yf[e] = fmaf(d1, (float)q[e], -m1);
+      if (yd) yd[e] = (double)d1 * (double)q[e] - (double)m1;
+    }
+  }
+}
+
+static int is_kquant(int type) { return type == OQ_Q4_K || type == OQ_Q5_K; }
+
 static void dequant_block(int type, const uint8_t* blk, uint16_t* y) {
+  if (is_kquant(type)) {
+    float v[256];
+    kq_dequant(type, blk, v, NULL);
+    for (int j = 0; j < 256; ++j) y[j] = oq_bf16_rne(v[j]);
+    return;
+  }
   double v[256];
   dequant_block_exact(type, blk, v);
   const int be = oq_block_elems(type);

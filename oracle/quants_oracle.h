@@ -26,6 +26,16 @@
  *   oq_ref_unpack    equality with the canonical dequant re-ordered into the
  *                    reference's output order.
  *   oq_matmul_f64    numpy float64 matmul on small shapes.
+ *   oq_dequant Q4_K / Q5_K (no reference code or vectors exist; ggml's
+ *                    published block layout): (i) the 6-bit scale/min fields
+ *                    decoded from bytes packed by an independent field-wise
+ *                    packer, over every (scale, min) pair at every group;
+ *                    (ii) blocks whose scales and mins reduce the K-quant to
+ *                    d' * (q - c) equal the Q8_0 oracle's dequant of the same
+ *                    codes, element by element (pins element order, nibble
+ *                    and qh bit placement, the sign of the min term); (iii)
+ *                    subnormal d / dmin against numpy's IEEE binary16; (iv)
+ *                    the single rounding (fmaf) against exact rationals.
  */
 #ifndef SPIRAL_QUANTS_ORACLE_H
 #define SPIRAL_QUANTS_ORACLE_H
@@ -37,7 +47,7 @@ extern "C" {
 #endif
 
 /* ggml type ids (the values ggml uses for these formats). */
-enum { OQ_Q4_0 = 2, OQ_Q8_0 = 8, OQ_Q6_K = 14 };
+enum { OQ_Q4_0 = 2, OQ_Q8_0 = 8, OQ_Q4_K = 12, OQ_Q5_K = 13, OQ_Q6_K = 14 };
 
 /* ---- scalar conversions ------------------------------------------------ */
 
@@ -90,7 +100,9 @@ int oq_block_elems(int type);
 /* Dequantize canonical rows into row-major bf16 out[n * ld_out + k].
  * Element value: bf16_rne(code * oq_fp16_device(d)) for Q4_0 (code = q-8)
  * and Q8_0; bf16_rne(oq_fp16_device(d) * sc * (q-32)) for Q6_K
- * (src/quants/tests/formats/q4_0.py:47-60, q8_0.py:48-58, q6_k.py:55-97).
+ * (src/quants/tests/formats/q4_0.py:47-60, q8_0.py:48-58, q6_k.py:55-97);
+ * bf16_rne(fmaf(d * scale, q, -dmin * min)) for Q4_K / Q5_K with IEEE d and
+ * dmin (the plan of src/quants/TODO.md:80-107 over ggml's block layout).
  * Returns 0, or -1 on a bad shape. */
 int oq_dequant(int type, const uint8_t* src, int64_t row_stride,
                int64_t n_rows, int64_t k, uint16_t* out, int64_t ld_out);

@@ -45,6 +45,8 @@ bool type_info(int type, size_t& bytes, int64_t& blck) {
     case SPIRAL_TYPE_Q4_0: bytes = kQ4_0Bytes; blck = kQ4_0Elems; return true;
     case SPIRAL_TYPE_Q8_0: bytes = kQ8_0Bytes; blck = kQ8_0Elems; return true;
     case SPIRAL_TYPE_Q6_K: bytes = kQ6_KBytes; blck = kQ6_KElems; return true;
+    case SPIRAL_TYPE_Q4_K: bytes = kQ4_KBytes; blck = 256; return true;
+    case SPIRAL_TYPE_Q5_K: bytes = kQ5_KBytes; blck = 256; return true;
     default: return false;
   }
 }
@@ -118,7 +120,7 @@ size_t elem_size(int type) { return type == SPIRAL_TYPE_F32 || type == SPIRAL_TY
 // Canonical byte o of a stack of matrices (each `rows` rows of nb blocks of
 // bb bytes) -> its planar byte offset.
 __host__ __device__ inline int64_t planar_offset(int type, int64_t rows, int64_t nb, int64_t o) {
-  const int64_t bb = type == SPIRAL_TYPE_Q4_0 ? kQ4_0Bytes : type == SPIRAL_TYPE_Q8_0 ? kQ8_0Bytes : kQ6_KBytes;
+  const int64_t bb = block_bytes(type);
   const int64_t mat = rows * nb * bb;
   const int64_t i = o / mat, r = o % mat;
   const int64_t blk = r / bb, j = r % bb;  // block index in the matrix, byte in the block
@@ -128,6 +130,12 @@ __host__ __device__ inline int64_t planar_offset(int type, int64_t rows, int64_t
     p = j < 2 ? tot * 16 + blk * 2 + j : blk * 16 + (j - 2);
   else if (type == SPIRAL_TYPE_Q8_0)
     p = j < 2 ? tot * 32 + blk * 2 + j : blk * 32 + (j - 2);
+  else if (type == SPIRAL_TYPE_Q4_K)
+    p = j < 16 ? tot * 128 + blk * 16 + j : blk * 128 + (j - 16);
+  else if (type == SPIRAL_TYPE_Q5_K)
+    p = j < 16   ? tot * 160 + blk * 16 + j
+        : j < 48 ? tot * 128 + blk * 32 + (j - 16)
+                 : blk * 128 + (j - 48);
   else
     p = j < 128   ? blk * 128 + j
         : j < 192 ? tot * 128 + blk * 64 + (j - 128)

@@ -15,16 +15,25 @@ namespace spiral {
 constexpr int kQ4_0Elems = 32, kQ4_0Bytes = 18;
 constexpr int kQ8_0Elems = 32, kQ8_0Bytes = 34;
 constexpr int kQ6_KElems = 256, kQ6_KBytes = 210;
+// K-quants with 6-bit scales and mins (ggml's block_q4_K / block_q5_K, the
+// formats src/quants/TODO.md:80-107 plans): d, dmin, scales[12], [qh[32]],
+// qs[128].
+constexpr int kQ4_KBytes = 144, kQ5_KBytes = 176;
 
-inline __host__ __device__ int block_elems(int type) {
-  return type == SPIRAL_TYPE_Q6_K ? kQ6_KElems
+constexpr __host__ __device__ bool is_kquant(int type) {
+  return type == SPIRAL_TYPE_Q4_K || type == SPIRAL_TYPE_Q5_K;
+}
+constexpr __host__ __device__ int block_elems(int type) {
+  return (type == SPIRAL_TYPE_Q6_K || is_kquant(type)) ? 256
          : (type == SPIRAL_TYPE_Q4_0 || type == SPIRAL_TYPE_Q8_0) ? 32
                                                                    : 0;
 }
-inline __host__ __device__ int block_bytes(int type) {
+constexpr __host__ __device__ int block_bytes(int type) {
   return type == SPIRAL_TYPE_Q4_0   ? kQ4_0Bytes
          : type == SPIRAL_TYPE_Q8_0 ? kQ8_0Bytes
          : type == SPIRAL_TYPE_Q6_K ? kQ6_KBytes
+         : type == SPIRAL_TYPE_Q4_K ? kQ4_KBytes
+         : type == SPIRAL_TYPE_Q5_K ? kQ5_KBytes
                                     : 0;
 }
 inline bool is_quant_type(int type) { return block_elems(type) != 0; }
@@ -58,6 +67,21 @@ struct PlanarQ6_K {
         d(reinterpret_cast<const uint16_t*>(ql + n_rows * nb * 208)) {}
 };
 
+// K-quants: the canonical block's first 16 bytes (fp16 d, fp16 dmin, the 12
+// packed scale/min bytes) stay together as one 16-byte "meta" entry, so a
+// lane takes every scale of a super-block in one aligned load.
+//   Q4_K: qs[n][nb][128] | meta[n][nb][16]
+//   Q5_K: qs[n][nb][128] | qh[n][nb][32] | meta[n][nb][16]
+struct PlanarKQ {
+  const uint8_t* qs;    // [n][nb][128]
+  const uint8_t* qh;    // [n][nb][32] (Q5_K)
+  const uint8_t* meta;  // [n][nb][16]
+  __host__ __device__ PlanarKQ(int type, const void* base, int64_t n_rows, int64_t nb)
+      : qs(static_cast<const uint8_t*>(base)),
+        qh(qs + n_rows * nb * 128),
+        meta(qs + n_rows * nb * (type == SPIRAL_TYPE_Q5_K ? 160 : 128)) {}
+};
+
 // ---- scalar decode ------------------------------------------------------------
 
 // Block-scale decode with the reference's device rule
@@ -68,6 +92,27 @@ __device__ __forceinline__ float fp16_scale(uint32_t h) {
   const uint32_t e = h & 0x7c00u;
   const uint32_t bits = ((h & 0x8000u) << 16) | (((h & 0x7fffu) << 13) + 0x38000000u);
   return __uint_as_float(e ? bits : 0u);
+}
+
+// IEEE binary16 -> float (subnormals keep their value): the K-quants' d and
+// dmin, decoded as ggml decodes them (v_cvt_f32_f16).
+__device__ __forceinline__ float fp16_ieee(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// 6-bit scale (bits 0..7) and min (bits 8..15) of group g (0..7) of a K-quant
+// super-block, from the dwords s0, s1, s2 of its 12 packed bytes:
+//   bytes 0..3   bits 0..5 scale of groups 0..3, bits 6..7 bits 4..5 of the
+//                scale of groups 4..7
+//   bytes 4..7   the same for the mins
+//   bytes 8..11  bits 0..3 of the scale (low nibble) and min (high nibble)
+//                of groups 4..7
+__device__ __forceinline__ uint32_t kq_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int g) {
+  const uint32_t sh = 8u * static_cast<uint32_t>(g & 3);
+  const uint32_t a = (s0 >> sh) & 0xffu, b = (s1 >> sh) & 0xffu, c = (s2 >> sh) & 0xffu;
+  const uint32_t sc = g < 4 ? (a & 63u) : ((c & 15u) | ((a >> 6) << 4));
+  const uint32_t mn = g < 4 ? (b & 63u) : ((c >> 4) | ((b >> 6) << 4));
+  return sc | (mn << 8);
 }
 
 // Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even.

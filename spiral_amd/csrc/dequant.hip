@@ -102,12 +102,16 @@ int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k, uint
   const uint32_t g32 = static_cast<uint32_t>(gpr), w32 = static_cast<uint32_t>(wpr);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* W = static_cast<const uint8_t*>(w);
-  if (type == SPIRAL_TYPE_Q4_0)
-    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q4_0>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out);
-  else if (type == SPIRAL_TYPE_Q8_0)
-    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q8_0>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out);
-  else
-    hipLaunchKernelGGL(dequant_kernel<SPIRAL_TYPE_Q6_K>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out);
+#define SPIRAL_DEQUANT(T) \
+  hipLaunchKernelGGL(dequant_kernel<T>, grid, dim3(256), 0, s, W, n_rows, nb, g32, w32, out, ld_out)
+  switch (type) {
+    case SPIRAL_TYPE_Q4_0: SPIRAL_DEQUANT(SPIRAL_TYPE_Q4_0); break;
+    case SPIRAL_TYPE_Q8_0: SPIRAL_DEQUANT(SPIRAL_TYPE_Q8_0); break;
+    case SPIRAL_TYPE_Q4_K: SPIRAL_DEQUANT(SPIRAL_TYPE_Q4_K); break;
+    case SPIRAL_TYPE_Q5_K: SPIRAL_DEQUANT(SPIRAL_TYPE_Q5_K); break;
+    default: SPIRAL_DEQUANT(SPIRAL_TYPE_Q6_K); break;
+  }
+#undef SPIRAL_DEQUANT
   return launch_status();
 }
 
@@ -137,9 +141,13 @@ int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k, const in
       hipLaunchKernelGGL((get_rows_kernel<T, false>), grid, dim3(256), 0, s, W, n_rows, nb,     \
                          g32, w32, ids, out, ld_out);                                           \
   } while (0)
-  if (type == SPIRAL_TYPE_Q4_0) SPIRAL_GET_ROWS(SPIRAL_TYPE_Q4_0);
-  else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_GET_ROWS(SPIRAL_TYPE_Q8_0);
-  else SPIRAL_GET_ROWS(SPIRAL_TYPE_Q6_K);
+  switch (type) {
+    case SPIRAL_TYPE_Q4_0: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q4_0); break;
+    case SPIRAL_TYPE_Q8_0: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q8_0); break;
+    case SPIRAL_TYPE_Q4_K: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q4_K); break;
+    case SPIRAL_TYPE_Q5_K: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q5_K); break;
+    default: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q6_K); break;
+  }
 #undef SPIRAL_GET_ROWS
   return launch_status();
 }

@@ -45,6 +45,30 @@ __device__ __forceinline__ void dequant8(const uint8_t* __restrict__ w, int64_t 
       v[j] = static_cast<float>(static_cast<int8_t>(q.x >> (8 * j))) * d;
       v[j + 4] = static_cast<float>(static_cast<int8_t>(q.y >> (8 * j))) * d;
     }
+  } else if constexpr (is_kquant(TYPE)) {
+    // Group j (32 elements) of a super-block: the low (j even) or high nibble
+    // of qs[32 (j / 2) + l], Q5_K adding bit j of qh[l] as bit 4; value
+    // fma(d * scale_j, q, -dmin * min_j), one rounding, then bf16 RNE.
+    const PlanarKQ P(TYPE, w, n_rows, nb);
+    const int64_t sb = g >> 5;
+    const int t = static_cast<int>(g & 31);
+    const int j = t >> 2, l0 = (t & 3) * 8;
+    const int64_t blk = n * nb + sb;
+    const uint2 q = *reinterpret_cast<const uint2*>(P.qs + blk * 128 + 32 * (j >> 1) + l0);
+    const uint4 m = *reinterpret_cast<const uint4*>(P.meta + blk * 16);
+    const uint32_t sm = kq_scale_min(m.y, m.z, m.w, j);
+    const float d1 = fp16_ieee(m.x & 0xffffu) * static_cast<float>(sm & 0xffu);
+    const float m1 = fp16_ieee(m.x >> 16) * static_cast<float>(sm >> 8);
+    const int ns = (j & 1) * 4;
+    uint2 hb = make_uint2(0u, 0u);
+    if constexpr (TYPE == SPIRAL_TYPE_Q5_K) hb = *reinterpret_cast<const uint2*>(P.qh + blk * 32 + l0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t c0 = ((q.x >> (8 * e + ns)) & 15u) | (((hb.x >> (8 * e + j)) & 1u) << 4);
+      const uint32_t c1 = ((q.y >> (8 * e + ns)) & 15u) | (((hb.y >> (8 * e + j)) & 1u) << 4);
+      v[e] = __builtin_fmaf(d1, static_cast<float>(c0), -m1);
+      v[e + 4] = __builtin_fmaf(d1, static_cast<float>(c1), -m1);
+    }
   } else {
     // Element e = 128h + 32j + l of a super-block takes the low (j < 2) or
     // high nibble of ql[64h + 32(j&1) + l], bits 2j..2j+1 of qh[32h + l] and
@@ -116,6 +140,13 @@ __device__ __forceinline__ Planes make_planes(const uint8_t* w, int64_t n_rows, 
     P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 32));
     P.d = buffer_rsrc(w + tot * 32, static_cast<uint32_t>(tot * 2));
     P.b = P.c = P.a;
+  } else if constexpr (is_kquant(TYPE)) {
+    // a: qs, b: qh (Q5_K), c: meta
+    constexpr int64_t kMeta = TYPE == SPIRAL_TYPE_Q5_K ? 160 : 128;
+    P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 128));
+    P.b = TYPE == SPIRAL_TYPE_Q5_K ? buffer_rsrc(w + tot * 128, static_cast<uint32_t>(tot * 32)) : P.a;
+    P.c = buffer_rsrc(w + tot * kMeta, static_cast<uint32_t>(tot * 16));
+    P.d = P.c;
   } else {
     P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 128));
     P.b = buffer_rsrc(w + tot * 128, static_cast<uint32_t>(tot * 64));
@@ -257,5 +288,55 @@ struct Piece<SPIRAL_TYPE_Q6_K> {
     o1 = make_uint4(o[4], o[5], o[6], o[7]);
   }
 };
+
+// K-quants: a 128-element step is half h = (k0 / 128) % 2 of super-block
+// k0 / 256; local piece pl covers elements 16 pl .. + 15 of the half, which
+// lie in group j = 4 h + pl / 2: qs bytes 64 h + 32 (pl / 4) + 16 (pl % 2)
+// .. + 15, nibble (pl / 2) % 2, Q5_K bit j of qh[16 (pl % 2) .. + 15]. The
+// piece carries the super-block's 16-byte meta (d, dmin, packed scales).
+template <int TYPE>
+struct PieceKQ {
+  uint4 q, meta, qh;
+  int grp;  // j
+  struct Addr {
+    uint32_t qs, qh, meta;
+    int jl, nib;  // pl / 2 and (pl / 2) % 2
+  };
+  static __device__ __forceinline__ Addr addr(int64_t n, int64_t nb, int pl) {
+    const uint32_t blk = static_cast<uint32_t>(n * nb);
+    return Addr{blk * 128u + 32u * (pl >> 2) + 16u * (pl & 1), blk * 32u + 16u * (pl & 1), blk * 16u, pl >> 1,
+                (pl >> 1) & 1};
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& A, int64_t k0) {
+    const uint32_t sb = static_cast<uint32_t>(k0 >> 8), h = static_cast<uint32_t>((k0 >> 7) & 1);
+    q = bload16(P.a, A.qs, sb * 128u + 64u * h);
+    meta = bload16(P.c, A.meta, sb * 16u);
+    if constexpr (TYPE == SPIRAL_TYPE_Q5_K) qh = bload16(P.b, A.qh, sb * 32u);
+    grp = 4 * static_cast<int>(h) + A.jl;
+  }
+  __device__ __forceinline__ void zero() { q = meta = qh = make_uint4(0u, 0u, 0u, 0u); grp = 0; }
+  __device__ __forceinline__ void dequant(const Addr& A, uint4& o0, uint4& o1) const {
+    const uint32_t sm = kq_scale_min(meta.y, meta.z, meta.w, grp);
+    const float d1 = fp16_ieee(meta.x & 0xffffu) * static_cast<float>(sm & 0xffu);
+    const float m1 = -(fp16_ieee(meta.x >> 16) * static_cast<float>(sm >> 8));
+    const uint32_t Q[4] = {q.x, q.y, q.z, q.w}, H[4] = {qh.x, qh.y, qh.z, qh.w};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t c = (A.nib ? (Q[i] >> 4) : Q[i]) & 0x0F0F0F0Fu;
+      if constexpr (TYPE == SPIRAL_TYPE_Q5_K) c |= ((H[i] >> grp) & 0x01010101u) << 4;
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(d1, static_cast<float>(c & 0xffu), m1),
+                             __builtin_fmaf(d1, static_cast<float>((c >> 8) & 0xffu), m1));
+      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(d1, static_cast<float>((c >> 16) & 0xffu), m1),
+                                 __builtin_fmaf(d1, static_cast<float>(c >> 24), m1));
+    }
+    o0 = make_uint4(o[0], o[1], o[2], o[3]);
+    o1 = make_uint4(o[4], o[5], o[6], o[7]);
+  }
+};
+template <>
+struct Piece<SPIRAL_TYPE_Q4_K> : PieceKQ<SPIRAL_TYPE_Q4_K> {};
+template <>
+struct Piece<SPIRAL_TYPE_Q5_K> : PieceKQ<SPIRAL_TYPE_Q5_K> {};
 
 }  // namespace spiral

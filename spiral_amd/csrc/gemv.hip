@@ -378,6 +378,118 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
   }
 };
 
+// ---- Q4_K / Q5_K --------------------------------------------------------------
+// Task t of a row = qs bytes 16 t .. 16 t + 15: super-block t / 8, chunk
+// c = (t / 2) % 4, half h = t % 2. Its low nibbles are elements
+// 64 c + 16 h + i of group 2 c, its high nibbles elements 64 c + 32 + 16 h + i
+// of group 2 c + 1 (i < 16); Q5_K adds bits 2 c and 2 c + 1 of
+// qh[16 h + i]. The super-block's 16-byte meta entry (fp16 d, fp16 dmin,
+// the packed 6-bit scales and mins) arrives in one load.
+// x entries per task: 4 x uint4 (group 2c's 16 x, then group 2c+1's);
+// sums: float2 (one per group).
+//   sum_i x_i (d sc q_i - dmin m) = d sc (sum x (128 + q) - 128 sum x) - dmin m sum x
+template <int TYPE>
+struct FmtKQ {
+  static constexpr int kTaskElems = 32, kE = 4;
+  static constexpr bool kQ5 = TYPE == SPIRAL_TYPE_Q5_K;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 8); }
+
+  struct Row {
+    const uint8_t* qs;
+    const uint8_t* qh;
+    const uint8_t* meta;
+  };
+  static __device__ __forceinline__ Row row(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r) {
+    const int64_t nb = k / 256, tot = n_rows * nb;
+    return Row{w + r * nb * 128, w + tot * 128 + r * nb * 32, w + tot * (kQ5 ? 160 : 128) + r * nb * 16};
+  }
+  struct Payload {
+    uint4 q, meta, qh;
+    uint32_t c2;  // 2 c: the task's low-nibble group
+  };
+  static __device__ __forceinline__ void load(Payload& p, const Row& R, int t) {
+    const uint32_t ut = static_cast<uint32_t>(t);
+    p.q = load_stream16(R.qs + ut * 16u);
+    p.meta = *reinterpret_cast<const uint4*>(R.meta + (ut >> 3) * 16u);
+    if constexpr (kQ5) p.qh = load_stream16(R.qh + (ut >> 3) * 32u + (ut & 1u) * 16u);
+    p.c2 = ut & 6u;
+  }
+  struct X {
+    uint4 xp[4];
+    float2 sum;
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) {
+    const uint8_t* e = lds + lds_task(t, kE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.xp[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+    x.sum = reinterpret_cast<const float2*>(lds + pad64(T) * kE * 16)[t];
+  }
+  // Item = task: 2 x 16 x (2 x 16 B) and the two sums.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const int T = static_cast<int>(k / 32);
+    float2* xs = reinterpret_cast<float2*>(lds + pad64(T) * kE * 16);
+    for (int b0 = threadIdx.x; b0 < T; b0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll][4];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int b = b0 + u * blockDim.x;
+        if (b < T) {
+          const uint4* src = reinterpret_cast<const uint4*>(x + (b >> 3) * 256 + ((b >> 1) & 3) * 64 + (b & 1) * 16);
+          v[u][0] = src[0];
+          v[u][1] = src[1];
+          v[u][2] = src[4];  // + 32 elements
+          v[u][3] = src[5];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int b = b0 + u * blockDim.x;
+        if (b >= T) break;
+        float s[2] = {0.0f, 0.0f};
+        uint8_t* dst = lds + lds_task(b, kE);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint4 q = v[u][i];
+          s[i >> 1] += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
+                       (bf16_lo(q.w) + bf16_hi(q.w));
+          *reinterpret_cast<uint4*>(dst + 1024 * i) = q;
+        }
+        xs[b] = make_float2(s[0], s[1]);
+      }
+    }
+  }
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
+    const uint32_t h[4] = {p.qh.x, p.qh.y, p.qh.z, p.qh.w};
+    float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (kQ5) {
+        lo |= ((h[i] >> p.c2) & 0x01010101u) << 4;
+        hi |= ((h[i] >> (p.c2 + 1)) & 0x01010101u) << 4;
+      }
+      const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
+      a0 = dot2(bf16_01(lo), (i & 1) ? el.z : el.x, a0);
+      a1 = dot2(bf16_23(lo), (i & 1) ? el.w : el.y, a1);
+      b0 = dot2(bf16_01(hi), (i & 1) ? eh.z : eh.x, b0);
+      b1 = dot2(bf16_23(hi), (i & 1) ? eh.w : eh.y, b1);
+    }
+    const uint32_t sl = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2));
+    const uint32_t sh = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2) + 1);
+    const float d = fp16_ieee(p.meta.x & 0xffffu), dmin = fp16_ieee(p.meta.x >> 16);
+    // bf16 (128 + q) against x: remove 128 * sum(x) per group.
+    const float gl = static_cast<float>(sl & 0xffu) * ((a0 + a1) - 128.0f * x.sum.x);
+    const float gh = static_cast<float>(sh & 0xffu) * ((b0 + b1) - 128.0f * x.sum.y);
+    const float ml = static_cast<float>(sl >> 8) * x.sum.x + static_cast<float>(sh >> 8) * x.sum.y;
+    return d * (gl + gh) - dmin * ml;
+  }
+};
+template <>
+struct Fmt<SPIRAL_TYPE_Q4_K> : FmtKQ<SPIRAL_TYPE_Q4_K> {};
+template <>
+struct Fmt<SPIRAL_TYPE_Q5_K> : FmtKQ<SPIRAL_TYPE_Q5_K> {};
+
 // ---- the kernel --------------------------------------------------------------
 
 template <int TYPE, int J>
@@ -547,6 +659,8 @@ int64_t gemv_max_k(int type) {
     case SPIRAL_TYPE_Q4_0: return max_k_of<SPIRAL_TYPE_Q4_0>();
     case SPIRAL_TYPE_Q8_0: return max_k_of<SPIRAL_TYPE_Q8_0>();
     case SPIRAL_TYPE_Q6_K: return max_k_of<SPIRAL_TYPE_Q6_K>();
+    case SPIRAL_TYPE_Q4_K: return max_k_of<SPIRAL_TYPE_Q4_K>();
+    case SPIRAL_TYPE_Q5_K: return max_k_of<SPIRAL_TYPE_Q5_K>();
     default: return 0;
   }
 }
@@ -558,6 +672,8 @@ int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, 
     case SPIRAL_TYPE_Q4_0: return launch_gemv<SPIRAL_TYPE_Q4_0>(w, n_rows, k, x, y, y_type, s);
     case SPIRAL_TYPE_Q8_0: return launch_gemv<SPIRAL_TYPE_Q8_0>(w, n_rows, k, x, y, y_type, s);
     case SPIRAL_TYPE_Q6_K: return launch_gemv<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_Q4_K: return launch_gemv<SPIRAL_TYPE_Q4_K>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_Q5_K: return launch_gemv<SPIRAL_TYPE_Q5_K>(w, n_rows, k, x, y, y_type, s);
     default: return SPIRAL_ERR_TYPE;
   }
 }

@@ -131,6 +131,19 @@ __global__ void to_planar_kernel(const uint8_t* __restrict__ src, int64_t stride
     q[0] = load16_u16(s + 1);
     q[1] = load16_u16(s + 9);
     reinterpret_cast<uint16_t*>(dst + total * 32)[i] = s[0];
+  } else if constexpr (is_kquant(TYPE)) {
+    // meta = canonical bytes 0..15; Q5_K qh = bytes 16..47; qs = the last 128.
+    constexpr bool Q5 = TYPE == SPIRAL_TYPE_Q5_K;
+    const uint16_t* s = reinterpret_cast<const uint16_t*>(src + n * stride + b * block_bytes(TYPE));
+    uint4* qs = reinterpret_cast<uint4*>(dst) + 8 * i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qs[j] = load16_u16(s + (Q5 ? 24 : 8) + 8 * j);
+    if constexpr (Q5) {
+      uint4* qh = reinterpret_cast<uint4*>(dst + total * 128) + 2 * i;
+      qh[0] = load16_u16(s + 8);
+      qh[1] = load16_u16(s + 16);
+    }
+    reinterpret_cast<uint4*>(dst + total * (Q5 ? 160 : 128))[i] = load16_u16(s);
   } else {
     const uint16_t* s = reinterpret_cast<const uint16_t*>(src + n * stride + b * kQ6_KBytes);
     uint4* ql = reinterpret_cast<uint4*>(dst) + 8 * i;
@@ -162,6 +175,18 @@ __global__ void from_planar_kernel(const uint8_t* __restrict__ src, int64_t n_ro
     o[0] = reinterpret_cast<const uint16_t*>(src + total * 32)[i];
     store16_u16(o + 1, q[0]);
     store16_u16(o + 9, q[1]);
+  } else if constexpr (is_kquant(TYPE)) {
+    constexpr bool Q5 = TYPE == SPIRAL_TYPE_Q5_K;
+    uint16_t* o = reinterpret_cast<uint16_t*>(dst + n * stride + b * block_bytes(TYPE));
+    const uint4* qs = reinterpret_cast<const uint4*>(src) + 8 * i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store16_u16(o + (Q5 ? 24 : 8) + 8 * j, qs[j]);
+    if constexpr (Q5) {
+      const uint4* qh = reinterpret_cast<const uint4*>(src + total * 128) + 2 * i;
+      store16_u16(o + 8, qh[0]);
+      store16_u16(o + 16, qh[1]);
+    }
+    store16_u16(o, reinterpret_cast<const uint4*>(src + total * (Q5 ? 160 : 128))[i]);
   } else {
     uint16_t* o = reinterpret_cast<uint16_t*>(dst + n * stride + b * kQ6_KBytes);
     const uint4* ql = reinterpret_cast<const uint4*>(src) + 8 * i;
@@ -241,12 +266,16 @@ int spiral_to_planar(int type, const void* src, int64_t src_row_stride, int64_t 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* in = static_cast<const uint8_t*>(src);
   uint8_t* out = static_cast<uint8_t*>(dst);
-  if (type == SPIRAL_TYPE_Q4_0)
-    hipLaunchKernelGGL(to_planar_kernel<SPIRAL_TYPE_Q4_0>, grid, dim3(256), 0, s, in, src_row_stride, n_rows, nb, out);
-  else if (type == SPIRAL_TYPE_Q8_0)
-    hipLaunchKernelGGL(to_planar_kernel<SPIRAL_TYPE_Q8_0>, grid, dim3(256), 0, s, in, src_row_stride, n_rows, nb, out);
-  else
-    hipLaunchKernelGGL(to_planar_kernel<SPIRAL_TYPE_Q6_K>, grid, dim3(256), 0, s, in, src_row_stride, n_rows, nb, out);
+#define SPIRAL_TO_PLANAR(T) \
+  hipLaunchKernelGGL(to_planar_kernel<T>, grid, dim3(256), 0, s, in, src_row_stride, n_rows, nb, out)
+  switch (type) {
+    case SPIRAL_TYPE_Q4_0: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q4_0); break;
+    case SPIRAL_TYPE_Q8_0: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q8_0); break;
+    case SPIRAL_TYPE_Q4_K: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q4_K); break;
+    case SPIRAL_TYPE_Q5_K: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q5_K); break;
+    default: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q6_K); break;
+  }
+#undef SPIRAL_TO_PLANAR
   return launch_status();
 }
 
@@ -262,12 +291,16 @@ int spiral_from_planar(int type, const void* src, int64_t n_rows, int64_t k, voi
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint8_t* in = static_cast<const uint8_t*>(src);
   uint8_t* out = static_cast<uint8_t*>(dst);
-  if (type == SPIRAL_TYPE_Q4_0)
-    hipLaunchKernelGGL(from_planar_kernel<SPIRAL_TYPE_Q4_0>, grid, dim3(256), 0, s, in, n_rows, nb, out, dst_row_stride);
-  else if (type == SPIRAL_TYPE_Q8_0)
-    hipLaunchKernelGGL(from_planar_kernel<SPIRAL_TYPE_Q8_0>, grid, dim3(256), 0, s, in, n_rows, nb, out, dst_row_stride);
-  else
-    hipLaunchKernelGGL(from_planar_kernel<SPIRAL_TYPE_Q6_K>, grid, dim3(256), 0, s, in, n_rows, nb, out, dst_row_stride);
+#define SPIRAL_FROM_PLANAR(T) \
+  hipLaunchKernelGGL(from_planar_kernel<T>, grid, dim3(256), 0, s, in, n_rows, nb, out, dst_row_stride)
+  switch (type) {
+    case SPIRAL_TYPE_Q4_0: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q4_0); break;
+    case SPIRAL_TYPE_Q8_0: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q8_0); break;
+    case SPIRAL_TYPE_Q4_K: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q4_K); break;
+    case SPIRAL_TYPE_Q5_K: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q5_K); break;
+    default: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q6_K); break;
+  }
+#undef SPIRAL_FROM_PLANAR
   return launch_status();
 }
 

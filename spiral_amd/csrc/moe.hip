@@ -281,6 +281,53 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
   }
 };
 
+// Q4_K / Q5_K: a 128-wide step is half h of super-block sb; piece g = qs
+// bytes 64 h + 32 (g / 2) + 16 (g % 2) .. + 15 of the super-block (chunk
+// c = 2 h + g / 2), both nibbles: MFMA s < 2 takes the low nibbles of bytes
+// 8 s .. 8 s + 7 (group 2 c), s >= 2 the high nibbles of bytes 8 (s - 2) ..
+// (group 2 c + 1); Q5_K adds bits 2 c / 2 c + 1 of the same positions of
+// qh[16 (g % 2) .. + 15]. The piece carries the super-block's meta entry.
+template <int TYPE>
+struct MoePieceKQ {
+  uint4 q, meta, qh;
+  int grp;                   // 2 c
+  float d0, m0, d1, m1;      // d * scale and -dmin * min of groups 2 c and 2 c + 1 (prep)
+  static __device__ __forceinline__ int local(int g, int s, int e) {
+    return 64 * (g >> 1) + (s < 2 ? 16 * (g & 1) + 8 * s : 32 + 16 * (g & 1) + 8 * (s - 2)) + e;
+  }
+  __device__ __forceinline__ void prep() {
+    const uint32_t sl = kq_scale_min(meta.y, meta.z, meta.w, grp);
+    const uint32_t sh = kq_scale_min(meta.y, meta.z, meta.w, grp + 1);
+    const float d = fp16_ieee(meta.x & 0xffffu), dm = fp16_ieee(meta.x >> 16);
+    d0 = d * static_cast<float>(sl & 0xffu);
+    m0 = -(dm * static_cast<float>(sl >> 8));
+    d1 = d * static_cast<float>(sh & 0xffu);
+    m1 = -(dm * static_cast<float>(sh >> 8));
+  }
+  __device__ __forceinline__ void zero() { q = meta = qh = make_uint4(0u, 0u, 0u, 0u); grp = 0; }
+  __device__ __forceinline__ uint4 dequant(int s) const {
+    const bool hi = s >= 2;
+    const uint32_t w0 = (s & 1) ? q.z : q.x, w1 = (s & 1) ? q.w : q.y;
+    const uint32_t h0 = (s & 1) ? qh.z : qh.x, h1 = (s & 1) ? qh.w : qh.y;
+    const float ds = hi ? d1 : d0, off = hi ? m1 : m0;
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t c = ((i ? w1 : w0) >> (hi ? 4 : 0)) & 0x0F0F0F0Fu;
+      if constexpr (TYPE == SPIRAL_TYPE_Q5_K) c |= (((i ? h1 : h0) >> (grp + (hi ? 1 : 0))) & 0x01010101u) << 4;
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>(c & 0xffu), off),
+                             __builtin_fmaf(ds, static_cast<float>((c >> 8) & 0xffu), off));
+      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>((c >> 16) & 0xffu), off),
+                                 __builtin_fmaf(ds, static_cast<float>(c >> 24), off));
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  }
+};
+template <>
+struct MoePiece<SPIRAL_TYPE_Q4_K> : MoePieceKQ<SPIRAL_TYPE_Q4_K> {};
+template <>
+struct MoePiece<SPIRAL_TYPE_Q5_K> : MoePieceKQ<SPIRAL_TYPE_Q5_K> {};
+
 constexpr int kMoeKC = 768;                   // k chunk of activations staged in LDS (3 pairs)
 constexpr int kMoeTok = 16;                   // tokens per pass (one MFMA row block)
 // Staged activation rows are padded by kAPad bf16 (64 bytes): an MFMA A
@@ -436,6 +483,54 @@ struct WStage<SPIRAL_TYPE_Q6_K> {
     pc.hs = 2 * g;
   }
 };
+
+// Q4_K / Q5_K pair: one super-block per row: qs 128 bytes (pitch 144), qh 32
+// (Q5_K, pitch 48), meta 16.
+template <int TYPE>
+struct WStageKQ {
+  static constexpr bool kQ5 = TYPE == SPIRAL_TYPE_Q5_K;
+  static constexpr int kQhOff = 64 * 144, kMetaOff = kQhOff + (kQ5 ? 64 * 48 : 0), kBytes = kMetaOff + 64 * 16;
+  struct Addr {
+    uint32_t q[2], qh, meta;
+  };
+  uint4 q[2];
+  uint32_t meta, h0, h1;
+  // thread t: qs bytes 16 (t % 8) of rows 32 i + t / 8; meta dword t % 4 and
+  // qh bytes 8 (t % 4) .. + 7 of row t / 4.
+  static __device__ __forceinline__ Addr addr(int64_t n0, int64_t n_rows, int64_t nb, int t) {
+    Addr a;
+    for (int i = 0; i < 2; ++i)
+      a.q[i] = static_cast<uint32_t>(min(n0 + 32 * i + t / 8, n_rows - 1) * nb * 128 + (t % 8) * 16);
+    const int64_t r4 = min(n0 + t / 4, n_rows - 1) * nb;
+    a.qh = static_cast<uint32_t>(r4 * 32 + (t % 4) * 8);
+    a.meta = static_cast<uint32_t>(r4 * 16 + (t % 4) * 4);
+    return a;
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t p, int64_t) {
+    const uint32_t sb = static_cast<uint32_t>(p);
+    for (int i = 0; i < 2; ++i) q[i] = bload16(P.a, a.q[i], sb * 128u);
+    meta = bload4(P.c, a.meta, sb * 16u);
+    if constexpr (kQ5) {
+      h0 = bload4(P.b, a.qh, sb * 32u);
+      h1 = bload4(P.b, a.qh + 4u, sb * 32u);
+    }
+  }
+  __device__ __forceinline__ void store(uint8_t* st, int t) const {
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(st + (32 * i + t / 8) * 144 + (t % 8) * 16) = q[i];
+    *reinterpret_cast<uint32_t*>(st + kMetaOff + (t / 4) * 16 + (t % 4) * 4) = meta;
+    if constexpr (kQ5) *reinterpret_cast<uint2*>(st + kQhOff + (t / 4) * 48 + (t % 4) * 8) = make_uint2(h0, h1);
+  }
+  static __device__ __forceinline__ void piece(MoePiece<TYPE>& pc, const uint8_t* st, int r, int h, int g) {
+    pc.q = *reinterpret_cast<const uint4*>(st + r * 144 + 64 * h + 32 * (g >> 1) + 16 * (g & 1));
+    pc.meta = *reinterpret_cast<const uint4*>(st + kMetaOff + r * 16);
+    if constexpr (kQ5) pc.qh = *reinterpret_cast<const uint4*>(st + kQhOff + r * 48 + 16 * (g & 1));
+    pc.grp = 4 * h + 2 * (g >> 1);
+  }
+};
+template <>
+struct WStage<SPIRAL_TYPE_Q4_K> : WStageKQ<SPIRAL_TYPE_Q4_K> {};
+template <>
+struct WStage<SPIRAL_TYPE_Q5_K> : WStageKQ<SPIRAL_TYPE_Q5_K> {};
 
 // Stage activations k in [c0, c0 + kMoeKC) of the pass's nt token rows in
 // MFMA order: item = 8 consecutive LDS positions (one lane group of one MFMA)
@@ -704,6 +799,30 @@ struct PieceAddr<SPIRAL_TYPE_Q6_K> {
     pc.hs = 2 * g;
   }
 };
+
+template <int TYPE>
+struct PieceAddrKQ {
+  uint32_t q, qh, meta;
+  int g;
+  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g_) {
+    g = g_;
+    q = static_cast<uint32_t>(row * nb * 128 + 32 * (g >> 1) + 16 * (g & 1));
+    qh = static_cast<uint32_t>(row * nb * 32 + 16 * (g & 1));
+    meta = static_cast<uint32_t>(row * nb * 16);
+  }
+  // Step st is half st % 2 of super-block st / 2.
+  __device__ __forceinline__ void load(MoePiece<TYPE>& pc, const Planes& P, int64_t st) const {
+    const uint32_t sb = static_cast<uint32_t>(st >> 1), hh = static_cast<uint32_t>(st & 1);
+    pc.q = bload16(P.a, q, sb * 128u + 64u * hh);
+    pc.meta = bload16(P.c, meta, sb * 16u);
+    if constexpr (TYPE == SPIRAL_TYPE_Q5_K) pc.qh = bload16(P.b, qh, sb * 32u);
+    pc.grp = 4 * static_cast<int>(hh) + 2 * (g >> 1);
+  }
+};
+template <>
+struct PieceAddr<SPIRAL_TYPE_Q4_K> : PieceAddrKQ<SPIRAL_TYPE_Q4_K> {};
+template <>
+struct PieceAddr<SPIRAL_TYPE_Q5_K> : PieceAddrKQ<SPIRAL_TYPE_Q5_K> {};
 
 // What one ring slot of the streaming form holds (a "unit"), loaded for one
 // 16-row group of the wave. Q4_0: a pair of k steps of all 16 rows, loaded
@@ -1275,6 +1394,8 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
   } while (0)
   if (type == SPIRAL_TYPE_Q4_0) SPIRAL_SKINNY(SPIRAL_TYPE_Q4_0);
   if (type == SPIRAL_TYPE_Q8_0) SPIRAL_SKINNY(SPIRAL_TYPE_Q8_0);
+  if (type == SPIRAL_TYPE_Q4_K) SPIRAL_SKINNY(SPIRAL_TYPE_Q4_K);
+  if (type == SPIRAL_TYPE_Q5_K) SPIRAL_SKINNY(SPIRAL_TYPE_Q5_K);
   SPIRAL_SKINNY(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_SKINNY
 }
@@ -1352,6 +1473,8 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   } while (0)
     if (type == SPIRAL_TYPE_Q4_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q4_0);
     if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q8_0);
+    if (type == SPIRAL_TYPE_Q4_K) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q4_K);
+    if (type == SPIRAL_TYPE_Q5_K) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q5_K);
     SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_MOE_STREAM
 #undef SPIRAL_MOE_STREAM_AS
@@ -1371,6 +1494,8 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   } while (0)
   if (type == SPIRAL_TYPE_Q4_0) SPIRAL_MOE(SPIRAL_TYPE_Q4_0);
   else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE(SPIRAL_TYPE_Q8_0);
+  else if (type == SPIRAL_TYPE_Q4_K) SPIRAL_MOE(SPIRAL_TYPE_Q4_K);
+  else if (type == SPIRAL_TYPE_Q5_K) SPIRAL_MOE(SPIRAL_TYPE_Q5_K);
   else SPIRAL_MOE(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_MOE
   return launch_status();

@@ -4,6 +4,9 @@ Distributions follow the benchmark workloads:
   Q4_0  fp16 d ~ U[1e-3, 2e-2], codes U{0..15}
   Q8_0  fp16 d ~ U[1e-3, 1e-2], int8 codes U{-127..127}
   Q6_K  ql, qh random bytes, int8 sub-scales U{1..63}, fp16 d ~ U[1e-4, 1e-3]
+  Q4_K / Q5_K  qs (and qh) random bytes, 6-bit scales and mins U{0..63},
+        fp16 d ~ U[1e-4, 1e-3], dmin ~ U[1e-5, 1e-4] (below 6.1e-5 it is an
+        fp16 subnormal, as it often is in real files)
   x     bf16 rounded from N(0, 1)
 Canonical layout: n_rows rows of k/block elements; row n starts at
 n * row_bytes. The generator is numpy's PCG64 (np.random.default_rng(seed)),
@@ -12,7 +15,7 @@ drawn field by field over the whole tensor.
 
 import numpy as np
 
-from . import BLOCK_BYTES, BLOCK_ELEMS, TYPE_Q4_0, TYPE_Q6_K, TYPE_Q8_0
+from . import BLOCK_BYTES, BLOCK_ELEMS, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0
 
 
 def bf16_bits(f32):
@@ -62,7 +65,57 @@ def make_q6_k(n_rows, k, rng, d_range=(1e-4, 1e-3), sc_range=(1, 63)):
     return blocks.reshape(-1)
 
 
-MAKERS = {TYPE_Q4_0: make_q4_0, TYPE_Q8_0: make_q8_0, TYPE_Q6_K: make_q6_k}
+def pack_scale_min(sc, mn):
+    """[..., 8] 6-bit scales and mins -> the [..., 12] packed K-quant bytes.
+
+    Field by field: bytes 0..3 and 4..7 hold groups 0..3's scale and min in
+    bits 0..5 and bits 4..5 of groups 4..7's in bits 6..7; bytes 8..11 hold
+    bits 0..3 of groups 4..7's scale (low nibble) and min (high nibble)."""
+    sc = np.asarray(sc, dtype=np.uint8)
+    mn = np.asarray(mn, dtype=np.uint8)
+    out = np.zeros(sc.shape[:-1] + (12,), dtype=np.uint8)
+    out[..., 0:4] = (sc[..., 0:4] & 63) | ((sc[..., 4:8] >> 4) << 6)
+    out[..., 4:8] = (mn[..., 0:4] & 63) | ((mn[..., 4:8] >> 4) << 6)
+    out[..., 8:12] = (sc[..., 4:8] & 15) | ((mn[..., 4:8] & 15) << 4)
+    return out
+
+
+def make_kquant(qtype, n_rows, k, rng, d_range=(1e-4, 1e-3), dmin_range=(1e-5, 1e-4)):
+    nb = n_rows * (k // 256)
+    bb = 176 if qtype == TYPE_Q5_K else 144
+    blocks = np.empty((nb, bb), dtype=np.uint8)
+    d = _fp16_bits(rng.uniform(d_range[0], d_range[1], nb))
+    dmin = _fp16_bits(rng.uniform(dmin_range[0], dmin_range[1], nb))
+    blocks[:, 0] = d & 0xFF
+    blocks[:, 1] = d >> 8
+    blocks[:, 2] = dmin & 0xFF
+    blocks[:, 3] = dmin >> 8
+    blocks[:, 4:16] = pack_scale_min(rng.integers(0, 64, (nb, 8)), rng.integers(0, 64, (nb, 8)))
+    blocks[:, 16:] = rng.integers(0, 256, (nb, bb - 16), dtype=np.uint8)
+    return blocks.reshape(-1)
+
+
+def pack_kquant(qtype, d_bits, dmin_bits, sc, mn, codes):
+    """One K-quant super-block from its fields: fp16 bit patterns d and dmin,
+    8 scales and 8 mins (0..63), 256 codes (0..15 for Q4_K, 0..31 for Q5_K).
+
+    Element 32 g + l takes the low (g even) or high (g odd) nibble of
+    qs[32 (g // 2) + l] and, for Q5_K, bit g of qh[l] as its bit 4."""
+    codes = np.asarray(codes, dtype=np.int64).reshape(8, 32)
+    qs = np.zeros(128, dtype=np.uint8)
+    qh = np.zeros(32, dtype=np.uint8)
+    for g in range(8):
+        nib = (codes[g] & 15).astype(np.uint8)
+        qs[32 * (g // 2):32 * (g // 2) + 32] |= nib << (4 * (g & 1))
+        qh |= (((codes[g] >> 4) & 1).astype(np.uint8) << g)
+    head = np.array([d_bits & 0xFF, d_bits >> 8, dmin_bits & 0xFF, dmin_bits >> 8], dtype=np.uint8)
+    parts = [head, pack_scale_min(sc, mn)] + ([qh] if qtype == TYPE_Q5_K else []) + [qs]
+    return np.concatenate(parts)
+
+
+MAKERS = {TYPE_Q4_0: make_q4_0, TYPE_Q8_0: make_q8_0, TYPE_Q6_K: make_q6_k,
+          TYPE_Q4_K: lambda n, k, rng: make_kquant(TYPE_Q4_K, n, k, rng),
+          TYPE_Q5_K: lambda n, k, rng: make_kquant(TYPE_Q5_K, n, k, rng)}
 
 
 def make_weights(qtype, n_rows, k, seed):

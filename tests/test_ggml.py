@@ -116,7 +116,7 @@ def weights(qtype, k, n, n_mat, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K, O.Q4_K, O.Q5_K])
 def test_set_get_round_trip_any_range(cuda, qtype):
     k, n, n_mat = O.BLOCK_ELEMS[qtype] * 3, 8, 3   # 24 blocks: each matrix a multiple of 16 bytes
     raw = weights(qtype, k, n, n_mat, 5)
@@ -218,7 +218,7 @@ def test_quantized_views(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K, O.Q4_K, O.Q5_K])
 @pytest.mark.parametrize("act", [ggml.TYPE_F32, ggml.TYPE_BF16])
 @pytest.mark.parametrize("m", [1, 6, 40])
 def test_mul_mat_node(cuda, qtype, act, m):
@@ -271,7 +271,7 @@ def test_mul_mat_broadcast_batches(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q6_K])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q6_K, O.Q5_K])
 def test_mul_mat_id_node(cuda, qtype):
     k, n, n_expert, top_k, n_tokens = O.BLOCK_ELEMS[qtype] * 2, 64, 6, 2, 10
     raws = [synth.make_weights(qtype, n, k, 60 + e) for e in range(n_expert)]
