@@ -18,7 +18,7 @@ Measurement
     copies of its weights to exceed the 256 MB Infinity Cache twice over, so
     successive launches read HBM, not the last-level cache.
   - A "step" is one launch of the workload's kernel(s). W warm-up steps, then
-    K steps captured in a HIP graph and replayed once untimed and once timed.
+    K steps captured in a HIP graph and replayed three times untimed and once timed.
     A HIP event pair on the replay stream brackets the timed replay:
     "ms_per_step" is its duration / K, "value" is K steps of algorithmic work
     over it (whole-job throughput, inputs resident in HBM), and
@@ -32,8 +32,14 @@ Measurement
     DIR rebuilds that file from DIR/{bench,copy}_{FETCH,WRITE}_SIZE/
     p_counter_collection.csv (rocprofv3 --pmc X --output-format csv -o p
     over this script, and over this script with --copy-calibration).
-  - "cpu_baseline": the CPU oracle's streaming dequantize-and-multiply over the
-    same canonical Q8_0 tensor, on the host's cores, repeated for ~10 s.
+  - "cpu_baseline" (the headline's, and one in each of the Q8_0 GEMV, Q4_0
+    dequant and Q4_0 GEMM workloads): oracle/cpu_baseline.c over the same
+    canonical tensors -- the reference's CPU semantics, vectorized (AVX-512 /
+    AVX2 clones picked at load) and spread over min(16, usable) host threads --
+    repeated for --cpu-seconds split across the legs; each records nproc,
+    the usable CPUs, OMP_NUM_THREADS and the CPU model.
+  - "step_us_replays": p10 / p50 / p90 of the step time over ten further
+    timed replays of the same K-launch graph (not part of "value").
 """
 
 import argparse
@@ -75,13 +81,15 @@ def copies_for(bytes_per_step):
 class Timer:
     """W eager warm-up launches, then K launches captured in one HIP graph.
 
-    The graph is replayed once untimed (upload), then once timed: a HIP event
+    The graph is replayed three times untimed (upload and settling), then once timed: a HIP event
     pair on the replay stream brackets the K launches, between two device
     synchronizations. Returns (wall seconds, event seconds) of the timed
     replay; event seconds / K is the mean duration of one step."""
 
-    def __init__(self, torch):
+    def __init__(self, torch, replays=10):
         self.torch = torch
+        self.replays = replays
+        self.spread = []
 
     def run(self, launch, steps, warmup):
         torch = self.torch
@@ -92,7 +100,8 @@ class Timer:
         with torch.cuda.graph(g):
             for i in range(steps):
                 launch(i)
-        g.replay()
+        for _ in range(3):  # upload, then two more untimed replays (clocks and caches settle)
+            g.replay()
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         start = torch.cuda.Event(enable_timing=True)
@@ -103,8 +112,20 @@ class Timer:
         end.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        ev = start.elapsed_time(end) * 1e-3
+        # Further timed replays of the same graph, for the spread of the step
+        # time (each a mean over K launches; not part of "value").
+        self.spread = []
+        for _ in range(self.replays):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            g.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            self.spread.append(a.elapsed_time(b) * 1e-3 / steps)
         del g
-        return wall, start.elapsed_time(end) * 1e-3
+        return wall, ev
 
 
 def traffic_table():
@@ -123,6 +144,8 @@ TRAFFIC_KERNELS = {
     "gemv_q8_0": (["gemv_kernel<8,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
     "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
     "gemv_q4_0": (["gemv_kernel<2,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "gemv_q4_k": (["gemv_kernel<12,"], 14336 * 4096 // 256 * 144 + 4096 * 2 + 14336 * 2),
+    "gemv_q5_k": (["gemv_kernel<13,"], 14336 * 4096 // 256 * 176 + 4096 * 2 + 14336 * 2),
     "mul_mat_q4_0_m4": (["skinny_kernel<2,"], 14336 * 4096 // 32 * 18 + 4 * 4096 * 2 + 4 * 14336 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
@@ -190,6 +213,52 @@ def copy_calibration(torch):
     print(json.dumps({"copy_calibration_bytes": n, "copies": 5}))
 
 
+def cpu_legs(args, results, inputs):
+    """CPU baselines of the same workloads (bounded samples of each), on the
+    host's cores: oracle/cpu_baseline.c, the reference's CPU semantics
+    (dequantize to bf16, fp32 products) vectorized and spread over OpenMP
+    threads. Each leg lands in its workload's entry as "cpu_baseline"."""
+    from oracle import oracle as O
+    host = O.host_cpu()
+    threads = min(16, host["affinity"] or 1)  # the GPU box's CPU share is 16 cores
+    legs = [n for n in ("gemv_q8_0", "dequant_q4_0", "gemm_q4_0") if n in inputs and n in results]
+    budget = args.cpu_seconds / max(1, len(legs))
+
+    def timed(fn):
+        fn()  # warm-up
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            passes += 1
+            if time.perf_counter() - t0 >= budget:
+                return passes, time.perf_counter() - t0
+
+    for name in legs:
+        base = {"cores": threads, "kind": "port", **host}
+        if name == "gemv_q8_0":
+            raw, x = inputs[name]
+            p, dt = timed(lambda: O.cb_gemv_q8_0(raw, 14336, 4096, x, threads))
+            base.update(value=raw.size * p / dt / 1e9, unit="GB/s",
+                        sample=f"{p} passes of the Q8_0 14336x4096 GEMV (canonical GGUF bytes, packed-weight GB/s), "
+                               f"{dt:.1f} s")
+        elif name == "dequant_q4_0":
+            (raw,) = inputs[name]
+            out = np.empty((4096, 4096), dtype=np.uint16)
+            p, dt = timed(lambda: O.cb_dequant_q4_0(raw, 4096, 4096, threads, out))
+            base.update(value=(raw.size + out.nbytes) * p / dt / 1e9, unit="GB/s",
+                        packed_GBps=raw.size * p / dt / 1e9,
+                        sample=f"{p} passes of the Q4_0 4096x4096 -> bf16 dequant (bytes in + out), {dt:.1f} s")
+        else:
+            raw, x = inputs[name]
+            p, dt = timed(lambda: O.cb_gemm_q4_0(raw, 4096, 4096, x, threads))
+            base.update(value=2.0 * 512 * 4096 * 4096 * p / dt / 1e9, unit="GFLOP/s",
+                        sample=f"{p} passes of the Q4_0 GEMM Y[512x4096] = X W^T, {dt:.1f} s")
+        r = results[name]
+        gpu = r["value"] * (1e3 if r["unit"] == "TFLOP/s" else 1.0)
+        base["gpu_over_cpu"] = gpu / base["value"]
+        r["cpu_baseline"] = base
+
+
 def main():
     args = parse()
     if args.write_traffic:
@@ -201,7 +270,7 @@ def main():
         sys.exit(2)
 
     import torch
-    from spiral_amd import ops, synth, TYPE_Q4_0, TYPE_Q6_K, TYPE_Q8_0, lib
+    from spiral_amd import ops, synth, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, lib
     from spiral_amd import row_bytes
 
     if not torch.cuda.is_available():
@@ -235,11 +304,16 @@ def main():
              "wall_ms_per_step": wall / steps * 1e3, "step_us": step * 1e6,
              "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                           "frac": achieved / peak}}
+        if timer.spread:
+            q = np.percentile(np.array(timer.spread) * 1e6, [10, 50, 90])
+            r["step_us_replays"] = {"p10": float(q[0]), "p50": float(q[1]), "p90": float(q[2]),
+                                    "replays": len(timer.spread), "launches_each": steps}
         if extra:
             r.update(extra)
         results[name] = r
 
     want = (lambda n: args.only in (None, n))
+    cpu_inputs = {}  # workload -> canonical inputs for its CPU baseline leg
 
     # --- Q8_0 GEMV (headline) -------------------------------------------------
     if want("gemv_q8_0"):
@@ -252,7 +326,7 @@ def main():
         record("gemv_q8_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q8_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
-        cpu_raw, cpu_x = raw, x
+        cpu_inputs["gemv_q8_0"] = (raw, x)
         del ws
 
     # --- Q6_K GEMV ------------------------------------------------------------
@@ -281,6 +355,22 @@ def main():
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
 
+    # --- Q4_K / Q5_K GEMV (the K-quants with 6-bit scales and mins) -------------
+    for qname, qt in (("q4_k", TYPE_Q4_K), ("q5_k", TYPE_Q5_K)):
+        wl = f"gemv_{qname}"
+        if not want(wl):
+            continue
+        n, k = 14336, 4096
+        wbytes = n * row_bytes(qt, k)
+        _, ws = upload_planar(qt, n, k, 21, copies_for(wbytes))
+        _, xd = x_dev(1, k, 22)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        wall, ev = timer.run(lambda i: ops.mul_mat(qt, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record(wl, wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": f"{qname.upper()} decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
+                "bytes_per_launch": wbytes, "copies": len(ws)})
+        del ws
+
     # --- Q4_0 small-batch product, m = 4 (speculative-decode batch) ---------------
     if want("mul_mat_q4_0_m4"):
         m, n, k = 4, 14336, 4096
@@ -302,7 +392,8 @@ def main():
         inb = n * row_bytes(TYPE_Q4_0, k)
         outb = n * k * 2
         copies = copies_for(inb + outb)
-        _, ws = upload_planar(TYPE_Q4_0, n, k, 0, copies)
+        raw0, ws = upload_planar(TYPE_Q4_0, n, k, 0, copies)
+        cpu_inputs["dequant_q4_0"] = (raw0,)
         outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
         wall, ev = timer.run(lambda i: ops.dequant(TYPE_Q4_0, ws[i % copies], n, k, out=outs[i % copies]),
                                steps, warmup)
@@ -333,8 +424,10 @@ def main():
         m, n, k = 512, 4096, 4096
         wbytes = n * row_bytes(TYPE_Q4_0, k)
         copies = copies_for(wbytes + m * k * 2 + m * n * 2)
-        _, ws = upload_planar(TYPE_Q4_0, n, k, 7, copies)
-        xs = [x_dev(m, k, 8 + c)[1] for c in range(copies)]
+        raw7, ws = upload_planar(TYPE_Q4_0, n, k, 7, copies)
+        xh = [x_dev(m, k, 8 + c) for c in range(copies)]
+        xs = [t for _, t in xh]
+        cpu_inputs["gemm_q4_0"] = (raw7, xh[0][0])
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         gws = ops.mul_mat_workspace(TYPE_Q4_0, n, k, m, dev)
         flops = 2.0 * m * n * k
@@ -358,16 +451,13 @@ def main():
         copies = max(2, int(np.ceil(2 * LLC_BYTES / (n_expert * (gu_per + dn_per)))))
 
         def stacked(n, k, per, seed):
-            out = []
-            base_raw = synth.make_weights(TYPE_Q4_0, n, k, seed)
-            base = ops.to_planar(TYPE_Q4_0, torch.from_numpy(base_raw).to(dev), n, k)
-            for _ in range(copies):
-                w = torch.empty(n_expert * per, dtype=torch.uint8, device=dev)
-                # distinct experts: a per-expert byte rotation of one seeded matrix
-                for e in range(n_expert):
-                    w[e * per:(e + 1) * per] = torch.roll(base, e * 7)
-                out.append(w)
-            return out
+            # every expert generated on its own (seed * 1000 + e), as the Q4_0
+            # workload defines a weight; the copies repeat the stack
+            first = torch.empty(n_expert * per, dtype=torch.uint8, device=dev)
+            for e in range(n_expert):
+                raw = synth.make_weights(TYPE_Q4_0, n, k, seed * 1000 + e)
+                first[e * per:(e + 1) * per] = ops.to_planar(TYPE_Q4_0, torch.from_numpy(raw).to(dev), n, k)
+            return [first] + [first.clone() for _ in range(copies - 1)]
 
         gus = stacked(inter2, hidden, gu_per, 10)
         dns = stacked(hidden, inter, dn_per, 11)
@@ -423,21 +513,10 @@ def main():
     roof = dict(head["roofline"])
 
     cpu = None
-    if head_name == "gemv_q8_0" and not args.no_cpu:
-        from oracle import oracle as O
-        threads = min(16, len(os.sched_getaffinity(0)))
-        n, k = 14336, 4096
-        O.quant_matmul_f32(O.Q8_0, cpu_raw, n, k, cpu_x, threads=threads)  # warm-up pass
-        passes, t0 = 0, time.perf_counter()
-        while True:
-            O.quant_matmul_f32(O.Q8_0, cpu_raw, n, k, cpu_x, threads=threads)
-            passes += 1
-            if time.perf_counter() - t0 >= args.cpu_seconds:
-                break
-        dt = time.perf_counter() - t0
-        cpu = {"value": cpu_raw.size * passes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-               "sample": f"{passes} full passes of the same Q8_0 14336x4096 GEMV (canonical GGUF bytes) "
-                         f"through the C oracle's streaming dequant+dot, OpenMP, {dt:.1f} s"}
+    if not args.no_cpu:
+        cpu_legs(args, results, cpu_inputs)
+        if head_name in results and "cpu_baseline" in results[head_name]:
+            cpu = results[head_name]["cpu_baseline"]
 
     line = {
         "metric": "quant GEMV packed-weight GB/s (% of HBM peak); dequant-GEMM TFLOP/s (% MFMA)",

@@ -274,3 +274,67 @@ def ref_shim(qtype):
 
 def cpu_count():
     return len(os.sched_getaffinity(0))
+
+
+# ---- the CPU baseline (oracle/cpu_baseline.c), timed by bench.py -------------
+
+_cb = None
+
+
+def cpu_baseline():
+    """ctypes handle on oracle/libcpu_baseline.so."""
+    global _cb
+    if _cb is None:
+        path = HERE / "libcpu_baseline.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        L = ctypes.CDLL(str(path))
+        L.cb_gemv_q8_0.argtypes = [_p, _i64, _i64, _p, _p, ctypes.c_int]
+        L.cb_gemv_q8_0.restype = ctypes.c_int
+        L.cb_dequant_q4_0.argtypes = [_p, _i64, _i64, _p, ctypes.c_int]
+        L.cb_dequant_q4_0.restype = ctypes.c_int
+        L.cb_gemm_q4_0.argtypes = [_p, _i64, _i64, _p, _i64, _p, ctypes.c_int]
+        L.cb_gemm_q4_0.restype = ctypes.c_int
+        _cb = L
+    return _cb
+
+
+def cb_gemv_q8_0(raw, n_rows, k, x_bf16, threads):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).reshape(-1)
+    y = np.empty(n_rows, dtype=np.float32)
+    if cpu_baseline().cb_gemv_q8_0(_ptr(raw), n_rows, k, _ptr(x), _ptr(y), threads) != 0:
+        raise ValueError("cb_gemv_q8_0: bad shape")
+    return y
+
+
+def cb_dequant_q4_0(raw, n_rows, k, threads, out=None):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty((n_rows, k), dtype=np.uint16) if out is None else out
+    if cpu_baseline().cb_dequant_q4_0(_ptr(raw), n_rows, k, _ptr(out), threads) != 0:
+        raise ValueError("cb_dequant_q4_0: bad shape")
+    return out
+
+
+def cb_gemm_q4_0(raw, n_rows, k, x_bf16, threads):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).reshape(-1, k)
+    y = np.empty((x.shape[0], n_rows), dtype=np.float32)
+    if cpu_baseline().cb_gemm_q4_0(_ptr(raw), n_rows, k, _ptr(x), x.shape[0], _ptr(y), threads) != 0:
+        raise ValueError("cb_gemm_q4_0: bad shape")
+    return y
+
+
+def host_cpu():
+    """What the CPU baseline ran on: logical CPUs, the usable set, OMP_NUM_THREADS, model."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"), "cpu_model": model}

@@ -368,3 +368,23 @@ def test_glu_oracle_closed_forms():
     for op in (O.GLU_REGLU, O.GLU_GEGLU, O.GLU_SWIGLU, O.GLU_GEGLU_ERF, O.GLU_GEGLU_QUICK):
         assert O.glu_f64(np.array([0.0, 5.0]), op)[0] == 0.0
         assert np.array_equal(O.glu_f64(h, op, swapped=True), O.glu_f64(np.concatenate([b, a]), op))
+
+
+# ---- the CPU baseline bench.py times (oracle/cpu_baseline.c) ---------------------
+
+def test_cpu_baseline_matches_the_oracle(oracle):
+    """The vectorized, multi-threaded CPU baseline computes what the oracle
+    computes: dequant bit for bit, products to fp32 summation order."""
+    from spiral_amd import synth
+    n, k = 67, 1024
+    q4 = synth.make_weights(O.Q4_0, n, k, 31)
+    assert np.array_equal(O.cb_dequant_q4_0(q4, n, k, 4), O.dequant(O.Q4_0, q4, n, k))
+    q8 = synth.make_weights(O.Q8_0, n, k, 32)
+    x = synth.make_x(1, k, 33)
+    ref = O.matmul_f64(O.dequant(O.Q8_0, q8, n, k), x)[0]
+    got = O.cb_gemv_q8_0(q8, n, k, x, 4)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+    xm = synth.make_x(9, k, 34)
+    ref = O.matmul_f64(O.dequant(O.Q4_0, q4, n, k), xm)
+    got = O.cb_gemm_q4_0(q4, n, k, xm, 4)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
