@@ -50,6 +50,8 @@ enum {
   SPIRAL_TYPE_Q4_K = 12,
   SPIRAL_TYPE_Q5_K = 13,
   SPIRAL_TYPE_Q6_K = 14,
+  SPIRAL_TYPE_IQ4_NL = 20,
+  SPIRAL_TYPE_IQ4_XS = 23,
   SPIRAL_TYPE_I32 = 26,
   SPIRAL_TYPE_BF16 = 30
 };
@@ -134,6 +136,9 @@ int quants_unpack_mmul_all(int type, const void* packed,
  *   Q5_K: qs[n_rows][k/256][128] | qh[..][32] | meta[..][16]                 *
  * (meta: a K-quant block's first 16 canonical bytes, fp16 d, fp16 dmin and  *
  * the 12 packed 6-bit scale/min bytes, kept together for one 16-byte load). *
+ *   IQ4_NL: as Q4_0: qs[n_rows][k/32][16] | d[n_rows][k/32]                  *
+ *   IQ4_XS: qs[n_rows][k/256][128] | meta[..][8] (fp16 d, scales_h,          *
+ *           scales_l[4]: the block's first 8 canonical bytes)                *
  * This is the GPU counterpart of the reference's load-time repack           *
  * (src/quants/TODO.md:303-334). Weight pointers below are planar and must be *
  * 16-byte aligned.                                                          *
@@ -158,7 +163,10 @@ int spiral_from_planar(int type, const void* src, int64_t n_rows, int64_t k,
  * the reference's unpack (src/quants/<fmt>/unpack.aie.h).
  * Q4_K / Q5_K (planned by the reference, src/quants/TODO.md:80-107, with no
  * code to match): bf16_rne(fma(d * scale, q, -dmin * min)), d and dmin IEEE
- * binary16 (subnormals keep their value, as in ggml), one float rounding. */
+ * binary16 (subnormals keep their value, as in ggml), one float rounding.
+ * IQ4_NL / IQ4_XS (planned, src/quants/TODO.md:109-124): bf16_rne(d *
+ * kv[index]) and bf16_rne(d * (ls - 32) * kv[index]) over ggml's 16-entry
+ * kvalues_iq4nl codebook, d IEEE binary16; each product is exact in fp32. */
 int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k,
                         uint16_t* out, int64_t ld_out, void* stream);
 

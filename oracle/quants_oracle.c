@@ -187,6 +187,8 @@ int oq_block_bytes(int type) {
     case OQ_Q6_K: return 210; /* src/quants/q6_k/layout.h:11-12 */
     case OQ_Q4_K: return 144; /* d, dmin, scales[12], qs[128] */
     case OQ_Q5_K: return 176; /* d, dmin, scales[12], qh[32], qs[128] */
+    case OQ_IQ4_NL: return 18; /* d, qs[16] */
+    case OQ_IQ4_XS: return 136; /* d, scales_h, scales_l[4], qs[128] */
     default: return 0;
   }
 }
@@ -198,6 +200,8 @@ int oq_block_elems(int type) {
     case OQ_Q6_K: return 256;
     case OQ_Q4_K: return 256;
     case OQ_Q5_K: return 256;
+    case OQ_IQ4_NL: return 32;
+    case OQ_IQ4_XS: return 256;
     default: return 0;
   }
 }
@@ -207,9 +211,13 @@ int oq_block_elems(int type) {
  * these to bf16 is the format's single rounding. */
 static void kq_dequant(int type, const uint8_t* blk, float* yf, double* yd);
 
+static void iq4_dequant(int type, const uint8_t* blk, double* y);
+
 static void dequant_block_exact(int type, const uint8_t* blk, double* y) {
   if (type == OQ_Q4_K || type == OQ_Q5_K) {
     kq_dequant(type, blk, NULL, y);
+  } else if (type == OQ_IQ4_NL || type == OQ_IQ4_XS) {
+    iq4_dequant(type, blk, y);
   } else if (type == OQ_Q4_0) {
     /* src/quants/tests/formats/q4_0.py:53-60: low nibbles are elements 0..15,
      * high nibbles 16..31, value (q - 8) * d. */
@@ -316,6 +324,38 @@ static void kq_dequant(int type, const uint8_t* blk, float* yf, double* yd) {
 }
 
 static int is_kquant(int type) { return type == OQ_Q4_K || type == OQ_Q5_K; }
+
+/* ---- IQ4_NL / IQ4_XS: 4-bit indices into a 16-entry codebook -----------
+ *
+ * The reference plans both (src/quants/TODO.md:109-124) with ggml's
+ * kvalues_iq4nl codebook and no code or vectors. Layout (ggml block_iq4_nl,
+ * block_iq4_xs): IQ4_NL {fp16 d, qs[16]} per 32 elements, element j the low
+ * (j < 16) or high nibble of qs[j % 16], value d * kv[index]; IQ4_XS {fp16 d,
+ * scales_h, scales_l[4], qs[128]} per 256: eight sub-blocks of 32 laid out as
+ * IQ4_NL blocks, sub-block b scaled by d * (ls - 32) with the 6-bit
+ * ls = (nibble b % 2 of scales_l[b / 2]) | (bits 2b..2b+1 of scales_h) << 4.
+ * d decodes as IEEE binary16, as for the K-quants. Every product is exact in
+ * float (d * (ls - 32) has at most 17 significant bits, kv at most 7), so
+ * the element is bf16_rne(exact product). */
+static const int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+static void iq4_dequant(int type, const uint8_t* blk, double* y) {
+  const float d = oq_fp16_ieee(le16(blk));
+  const int nsub = type == OQ_IQ4_XS ? 8 : 1;
+  const uint8_t* qs = blk + (type == OQ_IQ4_XS ? 8 : 2);
+  for (int b = 0; b < nsub; ++b) {
+    float dl = d;
+    if (type == OQ_IQ4_XS) {
+      const int sh = le16(blk + 2);
+      const int ls = ((blk[4 + b / 2] >> (4 * (b % 2))) & 15) | (((sh >> (2 * b)) & 3) << 4);
+      dl = d * (float)(ls - 32);
+    }
+    for (int j = 0; j < 16; ++j) {
+      y[32 * b + j] = (double)dl * kIq4Values[qs[16 * b + j] & 15];
+      y[32 * b + 16 + j] = (double)dl * kIq4Values[qs[16 * b + j] >> 4];
+    }
+  }
+}
 
 static void dequant_block(int type, const uint8_t* blk, uint16_t* y) {
   if (is_kquant(type)) {

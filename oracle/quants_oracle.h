@@ -36,6 +36,12 @@
  *                    and qh bit placement, the sign of the min term); (iii)
  *                    subnormal d / dmin against numpy's IEEE binary16; (iv)
  *                    the single rounding (fmaf) against exact rationals.
+ *   oq_dequant IQ4_NL / IQ4_XS (no reference code or vectors; ggml's layout
+ *                    and kvalues_iq4nl codebook): IQ4_NL blocks equal the Q8_0
+ *                    oracle on codes kv[index] with the same d; IQ4_XS
+ *                    sub-blocks equal IQ4_NL blocks with d' = d * (ls - 32);
+ *                    every 6-bit ls at every sub-block from an independent
+ *                    packer; subnormal d against numpy.
  */
 #ifndef SPIRAL_QUANTS_ORACLE_H
 #define SPIRAL_QUANTS_ORACLE_H
@@ -47,7 +53,7 @@ extern "C" {
 #endif
 
 /* ggml type ids (the values ggml uses for these formats). */
-enum { OQ_Q4_0 = 2, OQ_Q8_0 = 8, OQ_Q4_K = 12, OQ_Q5_K = 13, OQ_Q6_K = 14 };
+enum { OQ_Q4_0 = 2, OQ_Q8_0 = 8, OQ_Q4_K = 12, OQ_Q5_K = 13, OQ_Q6_K = 14, OQ_IQ4_NL = 20, OQ_IQ4_XS = 23 };
 
 /* ---- scalar conversions ------------------------------------------------ */
 
@@ -102,7 +108,9 @@ int oq_block_elems(int type);
  * and Q8_0; bf16_rne(oq_fp16_device(d) * sc * (q-32)) for Q6_K
  * (src/quants/tests/formats/q4_0.py:47-60, q8_0.py:48-58, q6_k.py:55-97);
  * bf16_rne(fmaf(d * scale, q, -dmin * min)) for Q4_K / Q5_K with IEEE d and
- * dmin (the plan of src/quants/TODO.md:80-107 over ggml's block layout).
+ * dmin (the plan of src/quants/TODO.md:80-107 over ggml's block layout);
+ * bf16_rne(d * kv[index]) for IQ4_NL and bf16_rne(d * (ls - 32) * kv[index])
+ * for IQ4_XS, IEEE d (src/quants/TODO.md:109-124, ggml's layout).
  * Returns 0, or -1 on a bad shape. */
 int oq_dequant(int type, const uint8_t* src, int64_t row_stride,
                int64_t n_rows, int64_t k, uint16_t* out, int64_t ld_out);

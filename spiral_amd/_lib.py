@@ -11,6 +11,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libspiral_quants.so"
 
 TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q6_K, TYPE_I32, TYPE_BF16 = 0, 1, 2, 8, 14, 26, 30
 TYPE_Q4_K, TYPE_Q5_K = 12, 13
+TYPE_IQ4_NL, TYPE_IQ4_XS = 20, 23
 
 STATUS = {
     0: "SPIRAL_OK", 1: "SPIRAL_ERR_SHAPE", 2: "SPIRAL_ERR_ALIGN", 3: "SPIRAL_ERR_NULL",

@@ -47,6 +47,8 @@ bool type_info(int type, size_t& bytes, int64_t& blck) {
     case SPIRAL_TYPE_Q6_K: bytes = kQ6_KBytes; blck = kQ6_KElems; return true;
     case SPIRAL_TYPE_Q4_K: bytes = kQ4_KBytes; blck = 256; return true;
     case SPIRAL_TYPE_Q5_K: bytes = kQ5_KBytes; blck = 256; return true;
+    case SPIRAL_TYPE_IQ4_NL: bytes = kIQ4_NLBytes; blck = 32; return true;
+    case SPIRAL_TYPE_IQ4_XS: bytes = kIQ4_XSBytes; blck = 256; return true;
     default: return false;
   }
 }
@@ -126,8 +128,10 @@ __host__ __device__ inline int64_t planar_offset(int type, int64_t rows, int64_t
   const int64_t blk = r / bb, j = r % bb;  // block index in the matrix, byte in the block
   const int64_t tot = rows * nb;
   int64_t p;
-  if (type == SPIRAL_TYPE_Q4_0)
+  if (type == SPIRAL_TYPE_Q4_0 || type == SPIRAL_TYPE_IQ4_NL)
     p = j < 2 ? tot * 16 + blk * 2 + j : blk * 16 + (j - 2);
+  else if (type == SPIRAL_TYPE_IQ4_XS)
+    p = j < 8 ? tot * 128 + blk * 8 + j : blk * 128 + (j - 8);
   else if (type == SPIRAL_TYPE_Q8_0)
     p = j < 2 ? tot * 32 + blk * 2 + j : blk * 32 + (j - 2);
   else if (type == SPIRAL_TYPE_Q4_K)

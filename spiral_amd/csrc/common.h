@@ -19,14 +19,20 @@ constexpr int kQ6_KElems = 256, kQ6_KBytes = 210;
 // formats src/quants/TODO.md:80-107 plans): d, dmin, scales[12], [qh[32]],
 // qs[128].
 constexpr int kQ4_KBytes = 144, kQ5_KBytes = 176;
+// Codebook formats (ggml's block_iq4_nl / block_iq4_xs, the formats
+// src/quants/TODO.md:109-124 plans): 4-bit indices into a 16-entry table.
+constexpr int kIQ4_NLBytes = 18, kIQ4_XSBytes = 136;
 
 constexpr __host__ __device__ bool is_kquant(int type) {
   return type == SPIRAL_TYPE_Q4_K || type == SPIRAL_TYPE_Q5_K;
 }
+constexpr __host__ __device__ bool is_iq4(int type) {
+  return type == SPIRAL_TYPE_IQ4_NL || type == SPIRAL_TYPE_IQ4_XS;
+}
 constexpr __host__ __device__ int block_elems(int type) {
-  return (type == SPIRAL_TYPE_Q6_K || is_kquant(type)) ? 256
-         : (type == SPIRAL_TYPE_Q4_0 || type == SPIRAL_TYPE_Q8_0) ? 32
-                                                                   : 0;
+  return (type == SPIRAL_TYPE_Q6_K || is_kquant(type) || type == SPIRAL_TYPE_IQ4_XS) ? 256
+         : (type == SPIRAL_TYPE_Q4_0 || type == SPIRAL_TYPE_Q8_0 || type == SPIRAL_TYPE_IQ4_NL) ? 32
+                                                                                                   : 0;
 }
 constexpr __host__ __device__ int block_bytes(int type) {
   return type == SPIRAL_TYPE_Q4_0   ? kQ4_0Bytes
@@ -34,6 +40,8 @@ constexpr __host__ __device__ int block_bytes(int type) {
          : type == SPIRAL_TYPE_Q6_K ? kQ6_KBytes
          : type == SPIRAL_TYPE_Q4_K ? kQ4_KBytes
          : type == SPIRAL_TYPE_Q5_K ? kQ5_KBytes
+         : type == SPIRAL_TYPE_IQ4_NL ? kIQ4_NLBytes
+         : type == SPIRAL_TYPE_IQ4_XS ? kIQ4_XSBytes
                                     : 0;
 }
 inline bool is_quant_type(int type) { return block_elems(type) != 0; }
@@ -113,6 +121,26 @@ __device__ __forceinline__ uint32_t kq_scale_min(uint32_t s0, uint32_t s1, uint3
   const uint32_t sc = g < 4 ? (a & 63u) : ((c & 15u) | ((a >> 6) << 4));
   const uint32_t mn = g < 4 ? (b & 63u) : ((c >> 4) | ((b >> 6) << 4));
   return sc | (mn << 8);
+}
+
+// IQ4 codebook entries of four 4-bit indices held one per byte of c (values
+// 0..15), as bytes kv + 128 (1..241) of ggml's kvalues_iq4nl
+// {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}:
+// one v_perm_b32 looks up entries 0..7, one entries 8..15, and a third picks
+// per byte by index bit 3.
+__device__ __forceinline__ uint32_t iq4_lut(uint32_t c) {
+  const uint32_t sel = c & 0x07070707u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x766A5D4Fu, 0x3F2D1801u, sel);  // entries 4..7 | 0..3
+  const uint32_t hi = __builtin_amdgcn_perm(0xF1D9C5B5u, 0xA6998D81u, sel);  // entries 12..15 | 8..11
+  return __builtin_amdgcn_perm(hi, lo, ((c >> 1) & 0x04040404u) | 0x03020100u);
+}
+
+// IQ4_XS sub-block scale d * (ls - 32) from a super-block's first 8 bytes
+// m = (d | scales_h << 16, scales_l[0..3]): ls = nibble b % 2 of
+// scales_l[b / 2] | bits 2b..2b+1 of scales_h << 4. Exact in fp32.
+__device__ __forceinline__ float iq4xs_scale(uint2 m, int b) {
+  const uint32_t ls = ((m.y >> (4 * b)) & 15u) | (((m.x >> (16 + 2 * b)) & 3u) << 4);
+  return fp16_ieee(m.x & 0xffffu) * static_cast<float>(static_cast<int>(ls) - 32);
 }
 
 // Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even.

@@ -109,6 +109,8 @@ int spiral_dequant_bf16(int type, const void* w, int64_t n_rows, int64_t k, uint
     case SPIRAL_TYPE_Q8_0: SPIRAL_DEQUANT(SPIRAL_TYPE_Q8_0); break;
     case SPIRAL_TYPE_Q4_K: SPIRAL_DEQUANT(SPIRAL_TYPE_Q4_K); break;
     case SPIRAL_TYPE_Q5_K: SPIRAL_DEQUANT(SPIRAL_TYPE_Q5_K); break;
+    case SPIRAL_TYPE_IQ4_NL: SPIRAL_DEQUANT(SPIRAL_TYPE_IQ4_NL); break;
+    case SPIRAL_TYPE_IQ4_XS: SPIRAL_DEQUANT(SPIRAL_TYPE_IQ4_XS); break;
     default: SPIRAL_DEQUANT(SPIRAL_TYPE_Q6_K); break;
   }
 #undef SPIRAL_DEQUANT
@@ -146,6 +148,8 @@ int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k, const in
     case SPIRAL_TYPE_Q8_0: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q8_0); break;
     case SPIRAL_TYPE_Q4_K: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q4_K); break;
     case SPIRAL_TYPE_Q5_K: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q5_K); break;
+    case SPIRAL_TYPE_IQ4_NL: SPIRAL_GET_ROWS(SPIRAL_TYPE_IQ4_NL); break;
+    case SPIRAL_TYPE_IQ4_XS: SPIRAL_GET_ROWS(SPIRAL_TYPE_IQ4_XS); break;
     default: SPIRAL_GET_ROWS(SPIRAL_TYPE_Q6_K); break;
   }
 #undef SPIRAL_GET_ROWS

@@ -45,6 +45,31 @@ __device__ __forceinline__ void dequant8(const uint8_t* __restrict__ w, int64_t 
       v[j] = static_cast<float>(static_cast<int8_t>(q.x >> (8 * j))) * d;
       v[j + 4] = static_cast<float>(static_cast<int8_t>(q.y >> (8 * j))) * d;
     }
+  } else if constexpr (is_iq4(TYPE)) {
+    // IQ4_NL: Q4_0's block with codebook values; IQ4_XS: eight such 32-element
+    // sub-blocks per super-block, sub-block b scaled by d * (ls_b - 32).
+    // Every product is exact in fp32.
+    int64_t qoff;
+    float dl;
+    if constexpr (TYPE == SPIRAL_TYPE_IQ4_NL) {
+      const int64_t b = n * nb + (g >> 2);
+      qoff = b * 16;
+      dl = fp16_ieee(reinterpret_cast<const uint16_t*>(w + n_rows * nb * 16)[b]);
+    } else {
+      const int64_t blk = n * nb + (g >> 5);
+      const int sub = static_cast<int>((g & 31) >> 2);
+      qoff = blk * 128 + 16 * sub;
+      dl = iq4xs_scale(reinterpret_cast<const uint2*>(w + n_rows * nb * 128)[blk], sub);
+    }
+    const int p = static_cast<int>(g & 3);
+    const uint2 q = *reinterpret_cast<const uint2*>(w + qoff + 8 * (p & 1));
+    const int shift = (p >> 1) * 4;
+    const uint32_t v0 = iq4_lut((q.x >> shift) & 0x0F0F0F0Fu), v1 = iq4_lut((q.y >> shift) & 0x0F0F0F0Fu);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = static_cast<float>(static_cast<int>((v0 >> (8 * j)) & 0xffu) - 128) * dl;
+      v[j + 4] = static_cast<float>(static_cast<int>((v1 >> (8 * j)) & 0xffu) - 128) * dl;
+    }
   } else if constexpr (is_kquant(TYPE)) {
     // Group j (32 elements) of a super-block: the low (j even) or high nibble
     // of qs[32 (j / 2) + l], Q5_K adding bit j of qh[l] as bit 4; value
@@ -128,7 +153,7 @@ template <int TYPE>
 __device__ __forceinline__ Planes make_planes(const uint8_t* w, int64_t n_rows, int64_t nb) {
   const int64_t tot = n_rows * nb;
   Planes P;
-  if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
+  if constexpr (TYPE == SPIRAL_TYPE_Q4_0 || TYPE == SPIRAL_TYPE_IQ4_NL) {
     P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 16));
     // d plane rounded up to whole dwords: a dword load of the last d (at a
     // 4-byte aligned address, so inside the same page) then reads it instead
@@ -140,6 +165,11 @@ __device__ __forceinline__ Planes make_planes(const uint8_t* w, int64_t n_rows, 
     P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 32));
     P.d = buffer_rsrc(w + tot * 32, static_cast<uint32_t>(tot * 2));
     P.b = P.c = P.a;
+  } else if constexpr (TYPE == SPIRAL_TYPE_IQ4_XS) {
+    P.a = buffer_rsrc(w, static_cast<uint32_t>(tot * 128));  // qs
+    P.c = buffer_rsrc(w + tot * 128, static_cast<uint32_t>(tot * 8));  // meta
+    P.b = P.a;
+    P.d = P.c;
   } else if constexpr (is_kquant(TYPE)) {
     // a: qs, b: qh (Q5_K), c: meta
     constexpr int64_t kMeta = TYPE == SPIRAL_TYPE_Q5_K ? 160 : 128;
@@ -338,5 +368,71 @@ template <>
 struct Piece<SPIRAL_TYPE_Q4_K> : PieceKQ<SPIRAL_TYPE_Q4_K> {};
 template <>
 struct Piece<SPIRAL_TYPE_Q5_K> : PieceKQ<SPIRAL_TYPE_Q5_K> {};
+
+// IQ4: 16 indices (one nibble of 16 qs bytes) -> codebook bytes (kv + 128)
+// -> fp16 pairs (1024 + kv + 128), times the scale minus 1152 scale: kv times
+// the scale, exact inside the FMA (the result has at most 24 bits).
+__device__ __forceinline__ void iq4_dequant16(const uint4& q, int hi, float df, uint4& o0, uint4& o1) {
+  const float off = -1152.0f * df;
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = iq4_lut((hi ? (w[i] >> 4) : w[i]) & 0x0F0F0F0Fu);
+    const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
+    const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
+    o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), df, off), __builtin_fmaf(static_cast<float>(a.y), df, off));
+    o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), df, off), __builtin_fmaf(static_cast<float>(b.y), df, off));
+  }
+  o0 = make_uint4(o[0], o[1], o[2], o[3]);
+  o1 = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+// IQ4_NL: piece 2b + h of a row is nibble h of block b's 16 qs bytes (as Q4_0).
+template <>
+struct Piece<SPIRAL_TYPE_IQ4_NL> {
+  uint4 q;
+  uint32_t d;
+  using Addr = Piece<SPIRAL_TYPE_Q4_0>::Addr;
+  static __device__ __forceinline__ Addr addr(int64_t n, int64_t nb, int pl) {
+    return Piece<SPIRAL_TYPE_Q4_0>::addr(n, nb, pl);
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& A, int64_t k0) {
+    const uint32_t kb = static_cast<uint32_t>(k0 >> 5);
+    q = bload16(P.a, A.qs, kb * 16u);
+    d = bload2(P.d, A.d, kb * 2u);
+  }
+  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
+  __device__ __forceinline__ void dequant(const Addr& A, uint4& o0, uint4& o1) const {
+    iq4_dequant16(q, A.hi, fp16_ieee(d), o0, o1);
+  }
+};
+
+// IQ4_XS: a 128-element step is half h of super-block k0 / 256; local piece pl
+// is nibble pl % 2 of sub-block 4 h + pl / 2's 16 qs bytes.
+template <>
+struct Piece<SPIRAL_TYPE_IQ4_XS> {
+  uint4 q;
+  uint2 meta;
+  int sub;
+  struct Addr {
+    uint32_t qs, meta;
+    int sl, hi;  // pl / 2 and pl % 2
+  };
+  static __device__ __forceinline__ Addr addr(int64_t n, int64_t nb, int pl) {
+    const uint32_t blk = static_cast<uint32_t>(n * nb);
+    return Addr{blk * 128u + 16u * (pl >> 1), blk * 8u, pl >> 1, pl & 1};
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& A, int64_t k0) {
+    const uint32_t sb = static_cast<uint32_t>(k0 >> 8), h = static_cast<uint32_t>((k0 >> 7) & 1);
+    q = bload16(P.a, A.qs, sb * 128u + 64u * h);
+    meta = make_uint2(bload4(P.c, A.meta, sb * 8u), bload4(P.c, A.meta + 4u, sb * 8u));
+    sub = 4 * static_cast<int>(h) + A.sl;
+  }
+  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); meta = make_uint2(0u, 0u); sub = 0; }
+  __device__ __forceinline__ void dequant(const Addr& A, uint4& o0, uint4& o1) const {
+    iq4_dequant16(q, A.hi, iq4xs_scale(meta, sub), o0, o1);
+  }
+};
 
 }  // namespace spiral

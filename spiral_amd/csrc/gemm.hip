@@ -151,9 +151,9 @@ __device__ __forceinline__ void mfma_step(f32x4_t (&acc)[4][4], const AFrag& a, 
 // kWRing<TYPE> weight-piece slots loaded kWRing + 1 steps ahead. Q6_K
 // pieces take twice the registers of the others, so its rings are shorter.
 template <int TYPE>
-constexpr int kARing = (TYPE == SPIRAL_TYPE_Q6_K || is_kquant(TYPE)) ? 2 : 4;
+constexpr int kARing = (TYPE == SPIRAL_TYPE_Q6_K || is_kquant(TYPE) || TYPE == SPIRAL_TYPE_IQ4_XS) ? 2 : 4;
 template <int TYPE>
-constexpr int kWRing = (TYPE == SPIRAL_TYPE_Q6_K || is_kquant(TYPE)) ? 2 : 4;
+constexpr int kWRing = (TYPE == SPIRAL_TYPE_Q6_K || is_kquant(TYPE) || TYPE == SPIRAL_TYPE_IQ4_XS) ? 2 : 4;
 
 template <int TYPE>
 struct Pipe {
@@ -375,6 +375,8 @@ int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, 
     case SPIRAL_TYPE_Q6_K: return launch_gemm<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
     case SPIRAL_TYPE_Q4_K: return launch_gemm<SPIRAL_TYPE_Q4_K>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
     case SPIRAL_TYPE_Q5_K: return launch_gemm<SPIRAL_TYPE_Q5_K>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
+    case SPIRAL_TYPE_IQ4_NL: return launch_gemm<SPIRAL_TYPE_IQ4_NL>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
+    case SPIRAL_TYPE_IQ4_XS: return launch_gemm<SPIRAL_TYPE_IQ4_XS>(w, n_rows, k, x, ldx, m, y, y_type, ldy, xp, s);
     default: return SPIRAL_ERR_TYPE;
   }
 }

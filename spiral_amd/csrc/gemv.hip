@@ -490,6 +490,112 @@ struct Fmt<SPIRAL_TYPE_Q4_K> : FmtKQ<SPIRAL_TYPE_Q4_K> {};
 template <>
 struct Fmt<SPIRAL_TYPE_Q5_K> : FmtKQ<SPIRAL_TYPE_Q5_K> {};
 
+// ---- IQ4_NL / IQ4_XS -------------------------------------------------------------
+// Task = 32 elements with one scale: an IQ4_NL block (16 qs bytes + fp16 d)
+// or an IQ4_XS sub-block (16 qs bytes; task t is sub-block t % 8 of
+// super-block t / 8, whose 8-byte meta entry (d, scales_h, scales_l) eight
+// lanes share). qs dword i holds elements 4i..4i+3 (low nibbles) and
+// 16+4i..16+4i+3 (high nibbles). Indices become codebook bytes kv + 128
+// (iq4_lut), then fp16 pairs (1024 + kv + 128) with one v_perm_b32 each,
+// multiplied against fp32 x with v_fma_mix_f32 (as Q8_0):
+//   sum kv x = sum (1152 + kv) x - 1152 sum x.
+// x entries per task: 8 x float4 (entries 0..3 the low-nibble elements of
+// qs dwords 0..3, entries 4..7 the high-nibble ones). Sum: float.
+template <int TYPE>
+struct FmtIQ4 {
+  static constexpr int kTaskElems = 32, kE = 8;
+  static constexpr bool kXS = TYPE == SPIRAL_TYPE_IQ4_XS;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 4); }
+
+  struct Row {
+    const uint8_t* qs;
+    const uint8_t* d;  // IQ4_NL: fp16 d plane; IQ4_XS: meta plane
+  };
+  static __device__ __forceinline__ Row row(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r) {
+    if constexpr (kXS) {
+      const int64_t nb = k / 256;
+      return Row{w + r * nb * 128, w + n_rows * nb * 128 + r * nb * 8};
+    } else {
+      const int64_t nb = k / 32;
+      return Row{w + r * nb * 16, w + n_rows * nb * 16 + r * nb * 2};
+    }
+  }
+  struct Payload {
+    uint4 q;
+    uint2 m;   // IQ4_XS meta; IQ4_NL: d in m.x
+    int sub;   // IQ4_XS sub-block
+  };
+  static __device__ __forceinline__ void load(Payload& p, const Row& R, int t) {
+    const uint32_t ut = static_cast<uint32_t>(t);
+    p.q = load_stream16(R.qs + ut * 16u);
+    if constexpr (kXS) {
+      p.m = *reinterpret_cast<const uint2*>(R.d + (ut >> 3) * 8u);
+      p.sub = static_cast<int>(ut & 7u);
+    } else {
+      p.m = make_uint2(*reinterpret_cast<const uint16_t*>(R.d + ut * 2u), 0u);
+      p.sub = 0;
+    }
+  }
+  struct X {
+    float4 x[8];
+    float sum;
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) {
+    const uint8_t* e = lds + lds_task(t, kE);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.x[i] = *reinterpret_cast<const float4*>(e + 1024 * i);
+    x.sum = reinterpret_cast<const float*>(lds + pad64(T) * kE * 16)[t];
+  }
+  // Item = task: its 32 x (4 x 16 B of bf16) widened to fp32, and their sum.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const int T = static_cast<int>(k / 32);
+    float* xs = reinterpret_cast<float*>(lds + pad64(T) * kE * 16);
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    for (int b0 = threadIdx.x; b0 < T; b0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll][4];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int b = b0 + u * blockDim.x;
+        if (b < T)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[u][i] = src[4 * b + i];
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int b = b0 + u * blockDim.x;
+        if (b >= T) break;
+        const uint32_t w[16] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w, v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w,
+                                v[u][2].x, v[u][2].y, v[u][2].z, v[u][2].w, v[u][3].x, v[u][3].y, v[u][3].z, v[u][3].w};
+        float s = 0.0f;
+        uint8_t* dst = lds + lds_task(b, kE);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {  // entry e: elements 4e .. 4e + 3 (e < 4: 0..15, else 16..31)
+          const float4 f = make_float4(bf16_lo(w[2 * e]), bf16_hi(w[2 * e]), bf16_lo(w[2 * e + 1]), bf16_hi(w[2 * e + 1]));
+          s += (f.x + f.y) + (f.z + f.w);
+          *reinterpret_cast<float4*>(dst + 1024 * e) = f;
+        }
+        xs[b] = s;
+      }
+    }
+  }
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 xl = x.x[i], xh = x.x[4 + i];
+      mix4(iq4_lut(w[i] & 0x0F0F0F0Fu), xl.x, xl.y, xl.z, xl.w, s0, s1);
+      mix4(iq4_lut((w[i] >> 4) & 0x0F0F0F0Fu), xh.x, xh.y, xh.z, xh.w, s0, s1);
+    }
+    const float sc = kXS ? iq4xs_scale(p.m, p.sub) : fp16_ieee(p.m.x);
+    return sc * ((s0 + s1) - 1152.0f * x.sum);
+  }
+};
+template <>
+struct Fmt<SPIRAL_TYPE_IQ4_NL> : FmtIQ4<SPIRAL_TYPE_IQ4_NL> {};
+template <>
+struct Fmt<SPIRAL_TYPE_IQ4_XS> : FmtIQ4<SPIRAL_TYPE_IQ4_XS> {};
+
 // ---- the kernel --------------------------------------------------------------
 
 template <int TYPE, int J>
@@ -661,6 +767,8 @@ int64_t gemv_max_k(int type) {
     case SPIRAL_TYPE_Q6_K: return max_k_of<SPIRAL_TYPE_Q6_K>();
     case SPIRAL_TYPE_Q4_K: return max_k_of<SPIRAL_TYPE_Q4_K>();
     case SPIRAL_TYPE_Q5_K: return max_k_of<SPIRAL_TYPE_Q5_K>();
+    case SPIRAL_TYPE_IQ4_NL: return max_k_of<SPIRAL_TYPE_IQ4_NL>();
+    case SPIRAL_TYPE_IQ4_XS: return max_k_of<SPIRAL_TYPE_IQ4_XS>();
     default: return 0;
   }
 }
@@ -674,6 +782,8 @@ int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, 
     case SPIRAL_TYPE_Q6_K: return launch_gemv<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, y, y_type, s);
     case SPIRAL_TYPE_Q4_K: return launch_gemv<SPIRAL_TYPE_Q4_K>(w, n_rows, k, x, y, y_type, s);
     case SPIRAL_TYPE_Q5_K: return launch_gemv<SPIRAL_TYPE_Q5_K>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_IQ4_NL: return launch_gemv<SPIRAL_TYPE_IQ4_NL>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_IQ4_XS: return launch_gemv<SPIRAL_TYPE_IQ4_XS>(w, n_rows, k, x, y, y_type, s);
     default: return SPIRAL_ERR_TYPE;
   }
 }

@@ -121,10 +121,17 @@ __global__ void to_planar_kernel(const uint8_t* __restrict__ src, int64_t stride
   if (i >= n_rows * nb) return;
   const int64_t n = i / nb, b = i % nb;
   const int64_t total = n_rows * nb;
-  if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
+  if constexpr (TYPE == SPIRAL_TYPE_Q4_0 || TYPE == SPIRAL_TYPE_IQ4_NL) {
     const uint16_t* s = reinterpret_cast<const uint16_t*>(src + n * stride + b * kQ4_0Bytes);
     reinterpret_cast<uint4*>(dst)[i] = load16_u16(s + 1);
     reinterpret_cast<uint16_t*>(dst + total * 16)[i] = s[0];
+  } else if constexpr (TYPE == SPIRAL_TYPE_IQ4_XS) {
+    // meta = canonical bytes 0..7 (d, scales_h, scales_l), qs = the last 128
+    const uint16_t* s = reinterpret_cast<const uint16_t*>(src + n * stride + b * kIQ4_XSBytes);
+    uint4* qs = reinterpret_cast<uint4*>(dst) + 8 * i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qs[j] = load16_u16(s + 4 + 8 * j);
+    reinterpret_cast<uint2*>(dst + total * 128)[i] = make_uint2(u16x2(s), u16x2(s + 2));
   } else if constexpr (TYPE == SPIRAL_TYPE_Q8_0) {
     const uint16_t* s = reinterpret_cast<const uint16_t*>(src + n * stride + b * kQ8_0Bytes);
     uint4* q = reinterpret_cast<uint4*>(dst) + 2 * i;
@@ -165,10 +172,17 @@ __global__ void from_planar_kernel(const uint8_t* __restrict__ src, int64_t n_ro
   if (i >= n_rows * nb) return;
   const int64_t n = i / nb, b = i % nb;
   const int64_t total = n_rows * nb;
-  if constexpr (TYPE == SPIRAL_TYPE_Q4_0) {
+  if constexpr (TYPE == SPIRAL_TYPE_Q4_0 || TYPE == SPIRAL_TYPE_IQ4_NL) {
     uint16_t* o = reinterpret_cast<uint16_t*>(dst + n * stride + b * kQ4_0Bytes);
     o[0] = reinterpret_cast<const uint16_t*>(src + total * 16)[i];
     store16_u16(o + 1, reinterpret_cast<const uint4*>(src)[i]);
+  } else if constexpr (TYPE == SPIRAL_TYPE_IQ4_XS) {
+    uint16_t* o = reinterpret_cast<uint16_t*>(dst + n * stride + b * kIQ4_XSBytes);
+    const uint4* qs = reinterpret_cast<const uint4*>(src) + 8 * i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store16_u16(o + 4 + 8 * j, qs[j]);
+    const uint2 m = reinterpret_cast<const uint2*>(src + total * 128)[i];
+    o[0] = m.x & 0xffff; o[1] = m.x >> 16; o[2] = m.y & 0xffff; o[3] = m.y >> 16;
   } else if constexpr (TYPE == SPIRAL_TYPE_Q8_0) {
     uint16_t* o = reinterpret_cast<uint16_t*>(dst + n * stride + b * kQ8_0Bytes);
     const uint4* q = reinterpret_cast<const uint4*>(src) + 2 * i;
@@ -273,6 +287,8 @@ int spiral_to_planar(int type, const void* src, int64_t src_row_stride, int64_t 
     case SPIRAL_TYPE_Q8_0: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q8_0); break;
     case SPIRAL_TYPE_Q4_K: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q4_K); break;
     case SPIRAL_TYPE_Q5_K: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q5_K); break;
+    case SPIRAL_TYPE_IQ4_NL: SPIRAL_TO_PLANAR(SPIRAL_TYPE_IQ4_NL); break;
+    case SPIRAL_TYPE_IQ4_XS: SPIRAL_TO_PLANAR(SPIRAL_TYPE_IQ4_XS); break;
     default: SPIRAL_TO_PLANAR(SPIRAL_TYPE_Q6_K); break;
   }
 #undef SPIRAL_TO_PLANAR
@@ -298,6 +314,8 @@ int spiral_from_planar(int type, const void* src, int64_t n_rows, int64_t k, voi
     case SPIRAL_TYPE_Q8_0: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q8_0); break;
     case SPIRAL_TYPE_Q4_K: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q4_K); break;
     case SPIRAL_TYPE_Q5_K: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q5_K); break;
+    case SPIRAL_TYPE_IQ4_NL: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_IQ4_NL); break;
+    case SPIRAL_TYPE_IQ4_XS: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_IQ4_XS); break;
     default: SPIRAL_FROM_PLANAR(SPIRAL_TYPE_Q6_K); break;
   }
 #undef SPIRAL_FROM_PLANAR

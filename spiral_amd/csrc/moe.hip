@@ -328,6 +328,41 @@ struct MoePiece<SPIRAL_TYPE_Q4_K> : MoePieceKQ<SPIRAL_TYPE_Q4_K> {};
 template <>
 struct MoePiece<SPIRAL_TYPE_Q5_K> : MoePieceKQ<SPIRAL_TYPE_Q5_K> {};
 
+// IQ4_NL / IQ4_XS: piece g = 32 elements with one scale (IQ4_NL block 4 kb + g;
+// IQ4_XS sub-block 4 h + g of the step's super-block half h), 16 qs bytes:
+// MFMA s takes qs dword s, low nibbles (elements 4s .. 4s + 3) then high
+// nibbles (16 + 4s ..), as Q4_0; indices become codebook values (iq4_lut).
+template <int TYPE>
+struct MoePieceIQ4 {
+  uint4 q;
+  uint2 meta;  // IQ4_NL: fp16 d in meta.x; IQ4_XS: d, scales_h, scales_l
+  int sub;     // IQ4_XS sub-block
+  float m, off;
+  static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
+  __device__ __forceinline__ void prep() {
+    m = TYPE == SPIRAL_TYPE_IQ4_XS ? iq4xs_scale(meta, sub) : fp16_ieee(meta.x & 0xffffu);
+    off = -1152.0f * m;
+  }
+  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); meta = make_uint2(0u, 0u); sub = 0; }
+  __device__ __forceinline__ uint4 dequant(int s) const {
+    const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t c = iq4_lut((i ? (w >> 4) : w) & 0x0F0F0F0Fu);
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), m, off), __builtin_fmaf(static_cast<float>(a.y), m, off));
+      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), m, off), __builtin_fmaf(static_cast<float>(b.y), m, off));
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+  }
+};
+template <>
+struct MoePiece<SPIRAL_TYPE_IQ4_NL> : MoePieceIQ4<SPIRAL_TYPE_IQ4_NL> {};
+template <>
+struct MoePiece<SPIRAL_TYPE_IQ4_XS> : MoePieceIQ4<SPIRAL_TYPE_IQ4_XS> {};
+
 constexpr int kMoeKC = 768;                   // k chunk of activations staged in LDS (3 pairs)
 constexpr int kMoeTok = 16;                   // tokens per pass (one MFMA row block)
 // Staged activation rows are padded by kAPad bf16 (64 bytes): an MFMA A
@@ -531,6 +566,50 @@ template <>
 struct WStage<SPIRAL_TYPE_Q4_K> : WStageKQ<SPIRAL_TYPE_Q4_K> {};
 template <>
 struct WStage<SPIRAL_TYPE_Q5_K> : WStageKQ<SPIRAL_TYPE_Q5_K> {};
+
+// IQ4_NL pair: Q4_0's staging (the planar layouts match).
+template <>
+struct WStage<SPIRAL_TYPE_IQ4_NL> : WStage<SPIRAL_TYPE_Q4_0> {
+  static __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_IQ4_NL>& pc, const uint8_t* st, int r, int h, int g) {
+    pc.q = *reinterpret_cast<const uint4*>(st + r * kQsPitch + (4 * h + g) * 16);
+    pc.meta = make_uint2(*reinterpret_cast<const uint16_t*>(st + kDOff + r * 16 + (4 * h + g) * 2), 0u);
+    pc.sub = 0;
+  }
+};
+
+// IQ4_XS pair: one super-block per row: qs 128 bytes (pitch 144) and meta 8.
+template <>
+struct WStage<SPIRAL_TYPE_IQ4_XS> {
+  static constexpr int kMetaOff = 64 * 144, kBytes = kMetaOff + 64 * 8;
+  struct Addr {
+    uint32_t q[2], meta;
+  };
+  uint4 q[2];
+  uint32_t meta;
+  // thread t: qs bytes 16 (t % 8) of rows 32 i + t / 8; meta dword t % 2 of
+  // row t / 4 (t % 4 >= 2 repeat it).
+  static __device__ __forceinline__ Addr addr(int64_t n0, int64_t n_rows, int64_t nb, int t) {
+    Addr a;
+    for (int i = 0; i < 2; ++i)
+      a.q[i] = static_cast<uint32_t>(min(n0 + 32 * i + t / 8, n_rows - 1) * nb * 128 + (t % 8) * 16);
+    a.meta = static_cast<uint32_t>(min(n0 + t / 4, n_rows - 1) * nb * 8 + (t % 2) * 4);
+    return a;
+  }
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t p, int64_t) {
+    const uint32_t sb = static_cast<uint32_t>(p);
+    for (int i = 0; i < 2; ++i) q[i] = bload16(P.a, a.q[i], sb * 128u);
+    meta = bload4(P.c, a.meta, sb * 8u);
+  }
+  __device__ __forceinline__ void store(uint8_t* st, int t) const {
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<uint4*>(st + (32 * i + t / 8) * 144 + (t % 8) * 16) = q[i];
+    if ((t % 4) < 2) *reinterpret_cast<uint32_t*>(st + kMetaOff + (t / 4) * 8 + (t % 2) * 4) = meta;
+  }
+  static __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_IQ4_XS>& pc, const uint8_t* st, int r, int h, int g) {
+    pc.q = *reinterpret_cast<const uint4*>(st + r * 144 + 64 * h + 16 * g);
+    pc.meta = *reinterpret_cast<const uint2*>(st + kMetaOff + r * 8);
+    pc.sub = 4 * h + g;
+  }
+};
 
 // Stage activations k in [c0, c0 + kMoeKC) of the pass's nt token rows in
 // MFMA order: item = 8 consecutive LDS positions (one lane group of one MFMA)
@@ -823,6 +902,38 @@ template <>
 struct PieceAddr<SPIRAL_TYPE_Q4_K> : PieceAddrKQ<SPIRAL_TYPE_Q4_K> {};
 template <>
 struct PieceAddr<SPIRAL_TYPE_Q5_K> : PieceAddrKQ<SPIRAL_TYPE_Q5_K> {};
+
+template <>
+struct PieceAddr<SPIRAL_TYPE_IQ4_NL> {
+  uint32_t q, d;
+  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g) {
+    q = static_cast<uint32_t>((row * nb + g) * 16);
+    d = static_cast<uint32_t>((row * nb + g) * 2);
+  }
+  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_IQ4_NL>& pc, const Planes& P, int64_t st) const {
+    pc.q = bload16(P.a, q, static_cast<uint32_t>(st) * 64u);
+    pc.meta = make_uint2(bload2(P.d, d, static_cast<uint32_t>(st) * 8u), 0u);
+    pc.sub = 0;
+  }
+};
+
+template <>
+struct PieceAddr<SPIRAL_TYPE_IQ4_XS> {
+  uint32_t q, meta;
+  int g;
+  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g_) {
+    g = g_;
+    q = static_cast<uint32_t>(row * nb * 128 + 16 * g);
+    meta = static_cast<uint32_t>(row * nb * 8);
+  }
+  // Step st is half st % 2 of super-block st / 2: sub-block 4 (st % 2) + g.
+  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_IQ4_XS>& pc, const Planes& P, int64_t st) const {
+    const uint32_t sb = static_cast<uint32_t>(st >> 1), hh = static_cast<uint32_t>(st & 1);
+    pc.q = bload16(P.a, q, sb * 128u + 64u * hh);
+    pc.meta = make_uint2(bload4(P.c, meta, sb * 8u), bload4(P.c, meta + 4u, sb * 8u));
+    pc.sub = 4 * static_cast<int>(hh) + g;
+  }
+};
 
 // What one ring slot of the streaming form holds (a "unit"), loaded for one
 // 16-row group of the wave. Q4_0: a pair of k steps of all 16 rows, loaded
@@ -1396,6 +1507,8 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
   if (type == SPIRAL_TYPE_Q8_0) SPIRAL_SKINNY(SPIRAL_TYPE_Q8_0);
   if (type == SPIRAL_TYPE_Q4_K) SPIRAL_SKINNY(SPIRAL_TYPE_Q4_K);
   if (type == SPIRAL_TYPE_Q5_K) SPIRAL_SKINNY(SPIRAL_TYPE_Q5_K);
+  if (type == SPIRAL_TYPE_IQ4_NL) SPIRAL_SKINNY(SPIRAL_TYPE_IQ4_NL);
+  if (type == SPIRAL_TYPE_IQ4_XS) SPIRAL_SKINNY(SPIRAL_TYPE_IQ4_XS);
   SPIRAL_SKINNY(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_SKINNY
 }
@@ -1475,6 +1588,8 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
     if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q8_0);
     if (type == SPIRAL_TYPE_Q4_K) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q4_K);
     if (type == SPIRAL_TYPE_Q5_K) SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q5_K);
+    if (type == SPIRAL_TYPE_IQ4_NL) SPIRAL_MOE_STREAM(SPIRAL_TYPE_IQ4_NL);
+    if (type == SPIRAL_TYPE_IQ4_XS) SPIRAL_MOE_STREAM(SPIRAL_TYPE_IQ4_XS);
     SPIRAL_MOE_STREAM(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_MOE_STREAM
 #undef SPIRAL_MOE_STREAM_AS
@@ -1496,6 +1611,8 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   else if (type == SPIRAL_TYPE_Q8_0) SPIRAL_MOE(SPIRAL_TYPE_Q8_0);
   else if (type == SPIRAL_TYPE_Q4_K) SPIRAL_MOE(SPIRAL_TYPE_Q4_K);
   else if (type == SPIRAL_TYPE_Q5_K) SPIRAL_MOE(SPIRAL_TYPE_Q5_K);
+  else if (type == SPIRAL_TYPE_IQ4_NL) SPIRAL_MOE(SPIRAL_TYPE_IQ4_NL);
+  else if (type == SPIRAL_TYPE_IQ4_XS) SPIRAL_MOE(SPIRAL_TYPE_IQ4_XS);
   else SPIRAL_MOE(SPIRAL_TYPE_Q6_K);
 #undef SPIRAL_MOE
   return launch_status();

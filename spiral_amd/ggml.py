@@ -9,8 +9,8 @@ libspiral_quants.so on the device; nothing here computes.
 
 import ctypes
 
-from ._lib import (TYPE_BF16, TYPE_F16, TYPE_F32, TYPE_I32, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K,  # noqa: F401
-                   TYPE_Q6_K, TYPE_Q8_0, check, lib)
+from ._lib import (TYPE_BF16, TYPE_F16, TYPE_F32, TYPE_I32, TYPE_IQ4_NL, TYPE_IQ4_XS, TYPE_Q4_0,  # noqa: F401
+                   TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, check, lib)
 
 MAX_DIMS, MAX_SRC, MAX_NAME, MAX_OP_PARAMS = 4, 10, 64, 16
 (OP_NONE, OP_GET_ROWS, OP_MUL_MAT, OP_MUL_MAT_ID, OP_VIEW, OP_RESHAPE, OP_PERMUTE,
@@ -23,7 +23,7 @@ FLAG_OUTPUT = 2  # ggml GGML_TENSOR_FLAG_OUTPUT
 TYPE_TRAITS = {
     TYPE_F32: (4, 1), TYPE_F16: (2, 1), TYPE_BF16: (2, 1), TYPE_I32: (4, 1),
     TYPE_Q4_0: (18, 32), TYPE_Q8_0: (34, 32), TYPE_Q6_K: (210, 256),
-    TYPE_Q4_K: (144, 256), TYPE_Q5_K: (176, 256),
+    TYPE_Q4_K: (144, 256), TYPE_Q5_K: (176, 256), TYPE_IQ4_NL: (18, 32), TYPE_IQ4_XS: (136, 256),
 }
 
 

@@ -7,6 +7,8 @@ Distributions follow the benchmark workloads:
   Q4_K / Q5_K  qs (and qh) random bytes, 6-bit scales and mins U{0..63},
         fp16 d ~ U[1e-4, 1e-3], dmin ~ U[1e-5, 1e-4] (below 6.1e-5 it is an
         fp16 subnormal, as it often is in real files)
+  IQ4_NL  fp16 d ~ U[1e-3, 1e-2], qs random bytes (codebook indices)
+  IQ4_XS  fp16 d ~ U[1e-4, 1e-3], 6-bit sub-block scales U{0..63}, qs random
   x     bf16 rounded from N(0, 1)
 Canonical layout: n_rows rows of k/block elements; row n starts at
 n * row_bytes. The generator is numpy's PCG64 (np.random.default_rng(seed)),
@@ -15,7 +17,8 @@ drawn field by field over the whole tensor.
 
 import numpy as np
 
-from . import BLOCK_BYTES, BLOCK_ELEMS, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0
+from . import (BLOCK_BYTES, BLOCK_ELEMS, TYPE_IQ4_NL, TYPE_IQ4_XS, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K,
+               TYPE_Q8_0)
 
 
 def bf16_bits(f32):
@@ -113,7 +116,58 @@ def pack_kquant(qtype, d_bits, dmin_bits, sc, mn, codes):
     return np.concatenate(parts)
 
 
+def pack_iq4_xs_scales(ls):
+    """[..., 8] 6-bit sub-block scales -> ([...] scales_h as uint16, [..., 4]
+    scales_l): sub-block b's low 4 bits in nibble b % 2 of scales_l[b // 2],
+    its high 2 bits in bits 2b..2b+1 of scales_h."""
+    ls = np.asarray(ls, dtype=np.int64)
+    lo = ls & 15
+    sl = (lo[..., 0::2] | (lo[..., 1::2] << 4)).astype(np.uint8)
+    sh = np.zeros(ls.shape[:-1], dtype=np.int64)
+    for b in range(8):
+        sh |= ((ls[..., b] >> 4) & 3) << (2 * b)
+    return sh.astype(np.uint16), sl
+
+
+def make_iq4_nl(n_rows, k, rng, d_range=(1e-3, 1e-2)):
+    nb = n_rows * (k // 32)
+    blocks = np.empty((nb, 18), dtype=np.uint8)
+    d = _fp16_bits(rng.uniform(d_range[0], d_range[1], nb))
+    blocks[:, 0] = d & 0xFF
+    blocks[:, 1] = d >> 8
+    blocks[:, 2:] = rng.integers(0, 256, (nb, 16), dtype=np.uint8)
+    return blocks.reshape(-1)
+
+
+def make_iq4_xs(n_rows, k, rng, d_range=(1e-4, 1e-3)):
+    nb = n_rows * (k // 256)
+    blocks = np.empty((nb, 136), dtype=np.uint8)
+    d = _fp16_bits(rng.uniform(d_range[0], d_range[1], nb))
+    sh, sl = pack_iq4_xs_scales(rng.integers(0, 64, (nb, 8)))
+    blocks[:, 0] = d & 0xFF
+    blocks[:, 1] = d >> 8
+    blocks[:, 2] = sh & 0xFF
+    blocks[:, 3] = sh >> 8
+    blocks[:, 4:8] = sl
+    blocks[:, 8:] = rng.integers(0, 256, (nb, 128), dtype=np.uint8)
+    return blocks.reshape(-1)
+
+
+def pack_iq4(qtype, d_bits, idx, ls=None):
+    """One IQ4_NL block (32 indices) or IQ4_XS super-block (256 indices and 8
+    scales) from its fields: element j of a 32-element (sub-)block is the low
+    (j < 16) or high nibble of its qs[j % 16]."""
+    idx = np.asarray(idx, dtype=np.int64).reshape(-1, 32)
+    qs = (idx[:, :16] | (idx[:, 16:] << 4)).astype(np.uint8).reshape(-1)
+    head = np.array([d_bits & 0xFF, d_bits >> 8], dtype=np.uint8)
+    if qtype == TYPE_IQ4_NL:
+        return np.concatenate([head, qs])
+    sh, sl = pack_iq4_xs_scales(np.asarray(ls).reshape(8))
+    return np.concatenate([head, np.array([int(sh) & 0xFF, int(sh) >> 8], dtype=np.uint8), sl, qs])
+
+
 MAKERS = {TYPE_Q4_0: make_q4_0, TYPE_Q8_0: make_q8_0, TYPE_Q6_K: make_q6_k,
+          TYPE_IQ4_NL: make_iq4_nl, TYPE_IQ4_XS: make_iq4_xs,
           TYPE_Q4_K: lambda n, k, rng: make_kquant(TYPE_Q4_K, n, k, rng),
           TYPE_Q5_K: lambda n, k, rng: make_kquant(TYPE_Q5_K, n, k, rng)}
 

@@ -116,7 +116,7 @@ def weights(qtype, k, n, n_mat, seed):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K, O.Q4_K, O.Q5_K])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K, O.Q4_K, O.Q5_K, O.IQ4_NL, O.IQ4_XS])
 def test_set_get_round_trip_any_range(cuda, qtype):
     k, n, n_mat = O.BLOCK_ELEMS[qtype] * 3, 8, 3   # 24 blocks: each matrix a multiple of 16 bytes
     raw = weights(qtype, k, n, n_mat, 5)
@@ -218,7 +218,7 @@ def test_quantized_views(cuda):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K, O.Q4_K, O.Q5_K])
+@pytest.mark.parametrize("qtype", [O.Q4_0, O.Q8_0, O.Q6_K, O.Q4_K, O.Q5_K, O.IQ4_NL, O.IQ4_XS])
 @pytest.mark.parametrize("act", [ggml.TYPE_F32, ggml.TYPE_BF16])
 @pytest.mark.parametrize("m", [1, 6, 40])
 def test_mul_mat_node(cuda, qtype, act, m):

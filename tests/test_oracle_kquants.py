@@ -160,3 +160,66 @@ def test_matmul_over_kquant_weights(oracle, qtype):
     x = synth.make_x(3, 768, 9)
     ref = _bf16_to_f64(x).reshape(3, 768) @ _bf16_to_f64(w).reshape(5, 768).T
     assert np.allclose(O.matmul_f64(w, x), ref, rtol=1e-12, atol=1e-12)
+
+
+# ---- IQ4_NL / IQ4_XS (codebook formats) -------------------------------------------
+#
+# The reference plans both (src/quants/TODO.md:109-124) with ggml's
+# kvalues_iq4nl codebook and holds no code or vectors; ggml is absent, so
+# parity with it is unpinned. The codebook is the format's own constant:
+KV = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+IQ4 = [O.IQ4_NL, O.IQ4_XS]
+
+
+def test_iq4_nl_equals_q8_0_on_the_codebook_values(oracle):
+    """IQ4_NL blocks equal the Q8_0 oracle's blocks with codes kv[index] and
+    the same d, element by element (nibble order, codebook, scaling); every
+    index appears, at every position across the blocks."""
+    rng = np.random.default_rng(11)
+    nblk = 64
+    idx = (np.arange(nblk)[:, None] + np.arange(32)[None, :]) % 16
+    d = synth._fp16_bits(rng.uniform(1e-3, 1e-1, nblk))
+    raw = np.concatenate([synth.pack_iq4(O.IQ4_NL, int(d[b]), idx[b]) for b in range(nblk)])
+    q8 = _q8_0_blocks(np.array(KV)[idx], 0).reshape(nblk, 34)
+    q8[:, 0] = d & 0xFF
+    q8[:, 1] = d >> 8
+    assert np.array_equal(O.dequant(O.IQ4_NL, raw, nblk, 32), O.dequant(O.Q8_0, q8.reshape(-1), nblk, 32))
+
+
+def test_iq4_xs_sub_blocks_equal_iq4_nl(oracle):
+    """An IQ4_XS super-block with d a power of two equals eight IQ4_NL blocks
+    with d' = d (ls - 32) (exact in fp16), for every 6-bit ls at every
+    sub-block position (an independent packer writes scales_l / scales_h)."""
+    rng = np.random.default_rng(12)
+    rows = []
+    nl = []
+    for t in range(64):
+        ls = (t + 9 * np.arange(8)) % 64
+        e = int(rng.integers(-14, -2))
+        d = np.float16(2.0 ** e)
+        idx = rng.integers(0, 16, 256)
+        rows.append(synth.pack_iq4(O.IQ4_XS, int(d.view(np.uint16)), idx, ls))
+        for b in range(8):
+            db = np.float16(float(d) * (int(ls[b]) - 32))
+            nl.append(synth.pack_iq4(O.IQ4_NL, int(db.view(np.uint16)), idx[32 * b:32 * b + 32]))
+    got = O.dequant(O.IQ4_XS, np.concatenate(rows), 64, 256)
+    ref = O.dequant(O.IQ4_NL, np.concatenate(nl), 64, 256)
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("qtype", IQ4)
+def test_iq4_subnormal_d_is_ieee_and_products_exact(oracle, qtype):
+    """d decodes as IEEE binary16 (subnormals kept) and every element is
+    bf16 of the exact product (rounded once, by torch from float64)."""
+    rng = np.random.default_rng(13)
+    for d_bits in (0x0001, 0x03FF, 0x8200, 0x3C00, 0x7BFF):
+        idx = rng.integers(0, 16, O.BLOCK_ELEMS[qtype])
+        ls = rng.integers(0, 64, 8)
+        raw = synth.pack_iq4(qtype, d_bits, idx, ls)
+        got = _bf16_to_f64(O.dequant(qtype, raw, 1, O.BLOCK_ELEMS[qtype]))[0]
+        d = float(np.uint16(d_bits).view(np.float16))
+        scale = np.repeat(ls - 32, 32) if qtype == O.IQ4_XS else 1
+        exact = d * scale * np.array(KV)[idx]
+        ref = torch.tensor(exact, dtype=torch.float64).to(torch.float32).to(torch.bfloat16).to(torch.float64).numpy()
+        assert np.array_equal(got, ref), hex(d_bits)
+        assert np.array_equal(O.dequant_exact(qtype, raw, 1, O.BLOCK_ELEMS[qtype])[0], exact)
