@@ -146,6 +146,8 @@ TRAFFIC_KERNELS = {
     "gemv_q4_0": (["gemv_kernel<2,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
     "gemv_q4_k": (["gemv_kernel<12,"], 14336 * 4096 // 256 * 144 + 4096 * 2 + 14336 * 2),
     "gemv_q5_k": (["gemv_kernel<13,"], 14336 * 4096 // 256 * 176 + 4096 * 2 + 14336 * 2),
+    "gemv_iq4_nl": (["gemv_kernel<20,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "gemv_iq4_xs": (["gemv_kernel<23,"], 14336 * 4096 // 256 * 136 + 4096 * 2 + 14336 * 2),
     "mul_mat_q4_0_m4": (["skinny_kernel<2,"], 14336 * 4096 // 32 * 18 + 4 * 4096 * 2 + 4 * 14336 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
@@ -270,7 +272,8 @@ def main():
         sys.exit(2)
 
     import torch
-    from spiral_amd import ops, synth, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, lib
+    from spiral_amd import (ops, synth, TYPE_IQ4_NL, TYPE_IQ4_XS, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K,
+                            TYPE_Q8_0, lib)
     from spiral_amd import row_bytes
 
     if not torch.cuda.is_available():
@@ -355,8 +358,8 @@ def main():
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
 
-    # --- Q4_K / Q5_K GEMV (the K-quants with 6-bit scales and mins) -------------
-    for qname, qt in (("q4_k", TYPE_Q4_K), ("q5_k", TYPE_Q5_K)):
+    # --- K-quant and IQ4 GEMV (6-bit scales and mins; the non-linear codebook) ---
+    for qname, qt in (("q4_k", TYPE_Q4_K), ("q5_k", TYPE_Q5_K), ("iq4_nl", TYPE_IQ4_NL), ("iq4_xs", TYPE_IQ4_XS)):
         wl = f"gemv_{qname}"
         if not want(wl):
             continue

@@ -1,8 +1,8 @@
 /*
  * spiral_quants.h -- C ABI of libspiral_quants.so, the MI355X (gfx950)
  * implementation of spiral's quantized-weight hot path: GGUF Q4_0 / Q8_0 /
- * Q6_K (and the K-quants Q4_K / Q5_K the reference plans) block
- * dequantization to bf16 and the dequant-fused matrix products behind a ggml
+ * Q6_K (and the Q4_K / Q5_K / IQ4_NL / IQ4_XS formats the reference plans)
+ * block dequantization to bf16 and the dequant-fused matrix products behind a ggml
  * backend's MUL_MAT / GET_ROWS / MUL_MAT_ID.
  *
  * Conventions
