@@ -450,7 +450,13 @@ int64_t oq_ref_record_count(int type, int64_t weights_rows, int64_t weights_cols
   const int rr = ref_record_rows(type);
   if (rr == 0 || weights_rows <= 0 || weights_cols <= 0) return 0;
   if (weights_rows % rr != 0 || weights_cols % 8 != 0) return 0;
-  return (weights_rows / rr) * (weights_cols / 8);
+  /* Shapes whose record stream overflows an int64 byte count are refused
+   * (the reference's product is unchecked there). */
+  int64_t records, bytes;
+  if (__builtin_mul_overflow(weights_rows / rr, weights_cols / 8, &records) ||
+      __builtin_mul_overflow(records, (int64_t)ref_record_bytes(type), &bytes))
+    return 0;
+  return records;
 }
 
 int64_t oq_ref_packed_bytes(int type, int64_t weights_rows, int64_t weights_cols) {

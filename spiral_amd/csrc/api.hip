@@ -6,6 +6,7 @@ int64_t gemv_max_k(int type);
 int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
          hipStream_t s);
 int64_t gemm_workspace_bytes(int64_t m, int64_t k);
+int64_t gemm_max_k();
 int gemm(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m,
          void* y, int y_type, int64_t ldy, void* workspace, hipStream_t s);
 bool skinny_fits(int type, int64_t n_rows, int64_t k, int64_t m);
@@ -36,9 +37,12 @@ int check_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_e
   if (n_expert <= 0 || n_rows <= 0 || k <= 0 || k % block_elems(type) != 0 || n_tokens < 0 || top_k <= 0)
     return SPIRAL_ERR_SHAPE;
   if (x_slots != 1 && x_slots != top_k) return SPIRAL_ERR_SHAPE;
-  if (expert_stride < spiral_tensor_bytes(type, n_rows, k) || expert_stride % 16 != 0) return SPIRAL_ERR_SHAPE;
-  if (n_tokens * top_k > INT32_MAX) return SPIRAL_ERR_SHAPE;
-  if (workspace_bytes < moe_workspace_bytes(n_expert, n_tokens * top_k)) return SPIRAL_ERR_CAPACITY;
+  const int64_t matrix_bytes = spiral_tensor_bytes(type, n_rows, k);
+  if (matrix_bytes == 0 || expert_stride < matrix_bytes || expert_stride % 16 != 0) return SPIRAL_ERR_SHAPE;
+  int64_t pairs = 0;
+  if (n_expert > INT32_MAX || __builtin_mul_overflow(n_tokens, top_k, &pairs) || pairs > INT32_MAX)
+    return SPIRAL_ERR_SHAPE;
+  if (workspace_bytes < moe_workspace_bytes(n_expert, pairs)) return SPIRAL_ERR_CAPACITY;
   if (!aligned16(w) || !aligned16(x) || k % 8 != 0) return SPIRAL_ERR_ALIGN;
   if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0 || (reinterpret_cast<uintptr_t>(workspace) & 3u) != 0)
     return SPIRAL_ERR_ALIGN;
@@ -54,7 +58,7 @@ int64_t spiral_mul_mat_workspace_bytes(int type, int64_t n_rows, int64_t k, int6
   if (!is_quant_type(type) || n_rows <= 0 || m <= 0 || k <= 0 || k % block_elems(type) != 0) return 0;
   if (m == 1 && k <= gemv_max_k(type)) return 0;
   if (skinny_fits(type, n_rows, k, m)) return 0;
-  return gemm_workspace_bytes(m, k);
+  return gemm_workspace_bytes(m, k);  // 0 past the GEMM's longest row: spiral_mul_mat refuses that shape
 }
 
 int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx,
@@ -64,9 +68,11 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uin
   if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
   if (w == nullptr || x == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
   if (n_rows <= 0 || m <= 0 || k <= 0 || k % block_elems(type) != 0) return SPIRAL_ERR_SHAPE;
-  if (ldx < k || ldy < n_rows) return SPIRAL_ERR_SHAPE;
+  if (ldx < k || ldy < n_rows || spiral_tensor_bytes(type, n_rows, k) == 0) return SPIRAL_ERR_SHAPE;
   if (!aligned16(w) || !aligned16(x) || ldx % 8 != 0) return SPIRAL_ERR_ALIGN;
   if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0) return SPIRAL_ERR_ALIGN;
+  const bool direct = (m == 1 && k <= gemv_max_k(type)) || skinny_fits(type, n_rows, k, m);
+  if (!direct && k > gemm_max_k()) return SPIRAL_ERR_SHAPE;
   const int64_t need = spiral_mul_mat_workspace_bytes(type, n_rows, k, m);
   if (need > 0) {
     if (workspace == nullptr) return SPIRAL_ERR_NULL;
@@ -76,16 +82,19 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uin
   int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (need == 0) {
-    if (m == 1) return gemv(type, w, n_rows, k, x, y, y_type, s);
+  if (direct) {
+    if (m == 1 && k <= gemv_max_k(type)) return gemv(type, w, n_rows, k, x, y, y_type, s);
     return skinny(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
   }
   return gemm(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, workspace, s);
 }
 
 int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens, int64_t top_k) {
-  if (n_expert <= 0 || n_tokens < 0 || top_k <= 0) return 0;
-  return moe_workspace_bytes(n_expert, n_tokens * top_k);
+  int64_t pairs = 0;
+  if (n_expert <= 0 || n_tokens < 0 || top_k <= 0 || n_expert > INT32_MAX ||
+      __builtin_mul_overflow(n_tokens, top_k, &pairs) || pairs > INT32_MAX)
+    return 0;  // a shape spiral_mul_mat_id refuses
+  return moe_workspace_bytes(n_expert, pairs);
 }
 
 int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,
@@ -147,7 +156,10 @@ int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride, int64_
 int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx, int64_t F, int64_t rows, float* y, int64_t ldy,
                void* stream) {
   if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
-  if (F < 0 || rows < 0 || ldx < 2 * F || ldy < F) return SPIRAL_ERR_SHAPE;
+  int64_t span = 0;
+  if (F < 0 || rows < 0 || F > INT64_MAX / 2 || ldx < 2 * F || ldy < F ||
+      __builtin_mul_overflow(rows, ldx > ldy ? ldx : ldy, &span))
+    return SPIRAL_ERR_SHAPE;
   if (F == 0 || rows == 0) return SPIRAL_OK;
   if (x == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
   if ((reinterpret_cast<uintptr_t>(x) & 3u) != 0 || (reinterpret_cast<uintptr_t>(y) & 3u) != 0)

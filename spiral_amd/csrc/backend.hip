@@ -585,7 +585,8 @@ int spiral_supports_op(const spiral_tensor* t) {
       const int64_t top_k = ids->ne[0], n_tokens = ids->ne[1];
       if (b->ne[0] != a->ne[0] || (b->ne[1] != 1 && b->ne[1] != top_k) || b->ne[2] != n_tokens) return 0;
       if (t->ne[0] != a->ne[1] || t->ne[1] != top_k || t->ne[2] != n_tokens || t->ne[3] != 1) return 0;
-      if (n_tokens * top_k > INT32_MAX) return 0;
+      int64_t pairs = 0;
+      if (__builtin_mul_overflow(n_tokens, top_k, &pairs) || pairs > INT32_MAX) return 0;
       return 1;
     }
     case SPIRAL_OP_GLU: {

@@ -43,6 +43,8 @@
 #include "dequant_impl.h"
 
 namespace spiral {
+int64_t gemm_max_k();
+
 namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -322,6 +324,7 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const uint8_t* __restric
 
 // Rows of X per launch: the packed chunk (rows rounded up to 16, times k
 // bf16) stays below 2 GiB so buffer offsets fit in 32 bits.
+// k is at most gemm_max_k(), so one M tile of packed X fits.
 int64_t chunk_rows(int64_t k) { return std::max<int64_t>(kBM, (kMaxBufferBytes / (k * 2)) / kBM * kBM); }
 
 template <int TYPE>
@@ -329,7 +332,8 @@ int launch_gemm(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int
                 int y_type, int64_t ldy, uint16_t* xp, hipStream_t s) {
   // Weight planes are addressed with 32-bit offsets (the largest plane is at
   // most 16/18 of the tensor).
-  if (spiral_tensor_bytes(TYPE, n_rows, k) >= kMaxBufferBytes * 2) return SPIRAL_ERR_SHAPE;
+  const int64_t wbytes = spiral_tensor_bytes(TYPE, n_rows, k);
+  if (wbytes == 0 || wbytes >= kMaxBufferBytes * 2 || k > gemm_max_k()) return SPIRAL_ERR_SHAPE;
   const int64_t chunk = chunk_rows(k);
   const int64_t tn = ceil_div(n_rows, kBN);
   const uint8_t* W = static_cast<const uint8_t*>(w);
@@ -357,8 +361,13 @@ int launch_gemm(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int
 
 }  // namespace
 
-// Workspace for the packed X of one launch chunk.
+// Longest row the GEMM takes: one 128-row tile of packed X must fit a
+// 32-bit buffer offset.
+int64_t gemm_max_k() { return kMaxBufferBytes / (2 * kBM); }
+
+// Workspace for the packed X of one launch chunk (0 when k > gemm_max_k()).
 int64_t gemm_workspace_bytes(int64_t m, int64_t k) {
+  if (k <= 0 || k > gemm_max_k()) return 0;
   const int64_t rows = std::min(m, chunk_rows(k));
   return ceil_div(rows, 16) * 16 * k * 2;
 }

@@ -220,7 +220,10 @@ int check_layout_args(int type, const void* a, const void* b, int64_t n_rows, in
   if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
   if (a == nullptr || b == nullptr) return SPIRAL_ERR_NULL;
   if (n_rows <= 0 || k <= 0 || k % block_elems(type) != 0) return SPIRAL_ERR_SHAPE;
-  if (stride < spiral_row_bytes(type, k) || (stride & 1)) return SPIRAL_ERR_SHAPE;
+  if (spiral_tensor_bytes(type, n_rows, k) == 0) return SPIRAL_ERR_SHAPE;
+  int64_t span = 0;
+  if (stride < spiral_row_bytes(type, k) || (stride & 1) || __builtin_mul_overflow(n_rows, stride, &span))
+    return SPIRAL_ERR_SHAPE;
   if ((reinterpret_cast<uintptr_t>(a) & 1) || (reinterpret_cast<uintptr_t>(b) & 1))
     return SPIRAL_ERR_ALIGN;
   return SPIRAL_OK;
@@ -257,15 +260,19 @@ int spiral_device_count(void) {
   return n;
 }
 
+// Both return 0 for a shape the type cannot hold and for byte counts past
+// INT64_MAX.
 int64_t spiral_row_bytes(int type, int64_t k) {
   const int be = block_elems(type);
   if (be == 0 || k <= 0 || k % be != 0) return 0;
-  return (k / be) * block_bytes(type);
+  int64_t bytes = 0;
+  return __builtin_mul_overflow(k / be, static_cast<int64_t>(block_bytes(type)), &bytes) ? 0 : bytes;
 }
 
 int64_t spiral_tensor_bytes(int type, int64_t n_rows, int64_t k) {
   if (n_rows <= 0) return 0;
-  return n_rows * spiral_row_bytes(type, k);
+  int64_t bytes = 0;
+  return __builtin_mul_overflow(n_rows, spiral_row_bytes(type, k), &bytes) ? 0 : bytes;
 }
 
 int spiral_to_planar(int type, const void* src, int64_t src_row_stride, int64_t n_rows,

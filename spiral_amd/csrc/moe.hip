@@ -1484,7 +1484,8 @@ int launch_skinny(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, i
 bool skinny_fits(int type, int64_t n_rows, int64_t k, int64_t m) {
   if (m < 2 || m > kMoeTok) return false;
   // weight planes are addressed with 32-bit offsets, past-the-end reads at 2^31
-  if (spiral_tensor_bytes(type, n_rows, k) >= (int64_t(1) << 31)) return false;
+  const int64_t wbytes = spiral_tensor_bytes(type, n_rows, k);
+  if (wbytes == 0 || wbytes >= (int64_t(1) << 31)) return false;
   return skinny_shape(type, n_rows, k, m).parts > 0;
 }
 
@@ -1564,7 +1565,8 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   const int f32 = y_type == SPIRAL_TYPE_F32;
   const bool glu = glu_op >= 0;
   // Weight planes of one expert are addressed with 32-bit offsets.
-  if (spiral_tensor_bytes(type, n_rows, k) >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
+  const int64_t wbytes = spiral_tensor_bytes(type, n_rows, k);
+  if (wbytes == 0 || wbytes >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
   if (glu && stream_lds_bytes(k) == 0) return SPIRAL_ERR_SHAPE;
   int32_t* offsets = nullptr;
   int32_t* list = nullptr;

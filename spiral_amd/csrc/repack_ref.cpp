@@ -60,9 +60,16 @@ constexpr Geometry kQ4_0{"Q4_0", 64, 288, 32, 18};
 constexpr Geometry kQ8_0{"Q8_0", 256, 2176, 32, 34};
 constexpr Geometry kQ6_K{"Q6_K", 256, 1680, 256, 210};
 
+// Records of a rows x cols matrix, 0 for a shape the format cannot hold and
+// for one whose record stream would not fit an int64 byte count (the
+// reference's product is unchecked there).
 int64_t record_count(const Geometry& g, int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0 || rows % g.record_rows != 0 || cols % 8 != 0) return 0;
-  return (rows / g.record_rows) * (cols / 8);
+  int64_t records = 0, bytes = 0;
+  if (__builtin_mul_overflow(rows / g.record_rows, cols / 8, &records) ||
+      __builtin_mul_overflow(records, static_cast<int64_t>(g.record_bytes), &bytes))
+    return 0;
+  return records;
 }
 
 struct Flags {
