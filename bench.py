@@ -443,7 +443,7 @@ def main():
         del ws, xs
 
     # --- Q4_0 MoE grouped GEMM ----------------------------------------------------
-    if want("moe_q4_0") or want("moe_gate_up_swiglu_q4_0"):
+    if want("moe_q4_0") or want("moe_gate_up_swiglu_q4_0") or want("moe_prefill_q4_0"):
         n_expert, hidden, inter2, inter = 128, 2048, 1536, 768
         n_tokens, top_k = 64, 8
         rng = np.random.default_rng(9)
@@ -503,6 +503,38 @@ def main():
                    {"workload": "Q4_0 MoE gate_up (128 experts of 1536x2048, 64 tokens, top-8) fused with SwiGLU "
                                 "into the [64][8][768] bf16 down-stage input; one step = one fused MUL_MAT_ID + GLU",
                     "bytes_per_launch": wbytes, "touched_experts": int(touched), "copies": copies})
+
+        # prefill-sized batch: 1024 tokens, top-8 (64 pairs an expert on average)
+        if want("moe_prefill_q4_0"):
+            pt = 1024
+            prng = np.random.default_rng(14)
+            pids = np.stack([prng.choice(n_expert, top_k, replace=False) for _ in range(pt)]).astype(np.int32)
+            pids_d = torch.from_numpy(pids).to(dev)
+            _, px1 = x_dev(pt, hidden, 15)
+            px1 = px1.view(pt, 1, hidden)
+            _, px2 = x_dev(pt * top_k, inter, 16)
+            px2 = px2.view(pt, top_k, inter)
+            py1 = torch.empty((pt, top_k, inter2), dtype=torch.bfloat16, device=dev)
+            py2 = torch.empty((pt, top_k, hidden), dtype=torch.bfloat16, device=dev)
+            pws1 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev)
+            pws2 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev)
+
+            def launch_prefill(i):
+                c = i % copies
+                ops.mul_mat_id(TYPE_Q4_0, gus[c], gu_per, n_expert, inter2, hidden, px1, pids_d, workspace=pws1,
+                               out=py1)
+                ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, px2, pids_d, workspace=pws2,
+                               out=py2)
+
+            wall, ev = timer.run(launch_prefill, steps, warmup)
+            ptouched = np.unique(pids).size
+            wbytes = ptouched * (gu_per + dn_per)
+            flops = 2.0 * pt * top_k * (inter2 * hidden + hidden * inter)
+            record("moe_prefill_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+                   {"workload": "Q4_0 MoE prefill: 128 experts (gate_up 1536x2048, down 2048x768), 1024 tokens, "
+                                "top-8 (64 pairs an expert on average); one step = gate_up + down MUL_MAT_ID",
+                    "bytes_per_launch": wbytes, "touched_experts": int(ptouched),
+                    "tflops": flops / (ev / steps) / 1e12, "copies": copies})
         del gus, dns
 
     if not results:

@@ -373,6 +373,7 @@ constexpr int kMoeTok = 16;                   // tokens per pass (one MFMA row b
 constexpr int kAPad = 32;
 constexpr int kMoeAPitch = kMoeKC + kAPad;    // bf16 per staged row
 constexpr int kFusedPairs = 1024;             // largest batch routed inside moe_kernel
+constexpr int kMaxRouteWaves = 16;            // waves of a routing workgroup (at most 1024 threads)
 constexpr int kStageAhead = 3;                // weight pairs in flight in registers
 static_assert(kMoeKC % 256 == 0, "activation chunks hold whole weight pairs");
 
@@ -1025,8 +1026,10 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
 };
 
 // Routing shared by both forms: the expert's pairs as [begin, end) of lst.
-// Fused (offsets == nullptr): scan ids into s_list; expert 0's workgroups
-// also clear the rows of pairs routed nowhere over columns [c0, c1).
+// Fused (offsets == nullptr): a stable compaction of the pairs routed to e
+// into s_list, in pair order, so every workgroup of the expert holds the same
+// list (pass lanes split it between workgroups); expert 0's workgroups also
+// clear the rows of pairs routed nowhere over columns [c0, c1).
 template <bool F32_OUT>
 __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
                                           int64_t e, const int32_t* __restrict__ offsets,
@@ -1034,12 +1037,22 @@ __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32
                                           void* __restrict__ y, int64_t n_rows, int64_t c0, int64_t c1, int tid,
                                           int nthreads, int32_t& begin, int32_t& end, const int32_t*& lst) {
   if (offsets == nullptr) {
-    if (tid == 0) s_n = 0;
-    __syncthreads();
-    for (int32_t p = tid; p < n_pairs; p += nthreads) {
-      const int32_t id = ids[p];
-      if (id == e) s_list[atomicAdd(&s_n, 1)] = p;
-      if (e == 0 && (id < 0 || id >= n_expert)) {
+    __shared__ int32_t s_wave_hits[kMaxRouteWaves];
+    const int wave = tid >> 6, lane = tid & 63, n_waves = nthreads >> 6;
+    int32_t base = 0;
+    for (int32_t p0 = 0; p0 < n_pairs; p0 += nthreads) {  // the same trip count in every thread
+      const int32_t p = p0 + tid;
+      const int32_t id = p < n_pairs ? ids[p] : -1;
+      const uint64_t hits = __ballot(id == e);
+      if (lane == 0) s_wave_hits[wave] = __popcll(hits);
+      __syncthreads();
+      int32_t before = 0, chunk = 0;
+      for (int v = 0; v < n_waves; ++v) {
+        before += v < wave ? s_wave_hits[v] : 0;
+        chunk += s_wave_hits[v];
+      }
+      if (id == e) s_list[base + before + __popcll(hits & ((uint64_t(1) << lane) - 1))] = p;
+      if (p < n_pairs && e == 0 && (id < 0 || id >= n_expert)) {
         for (int64_t c = c0; c < min(c1, n_rows); ++c) {
           if constexpr (F32_OUT)
             static_cast<float*>(y)[p * n_rows + c] = 0.0f;
@@ -1047,10 +1060,12 @@ __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32
             static_cast<uint16_t*>(y)[p * n_rows + c] = 0;
         }
       }
+      base += chunk;
+      __syncthreads();  // s_wave_hits is rewritten by the next chunk
     }
-    __syncthreads();
+    if (tid == 0) s_n = base;
     begin = 0;
-    end = s_n;
+    end = base;
     lst = s_list;
   } else {
     begin = offsets[e];
@@ -1061,28 +1076,38 @@ __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32
 
 // GLU: the fused form above (glu_op, swapped); the output then has n_rows / 2
 // columns and the workgroups' row ranges are over those features.
-template <int TYPE, bool F32_OUT, bool GLU>
+//
+// TB: MFMA row blocks per pass. A pass takes up to 16 TB of the expert's
+// routed tokens, so every dequantized weight feeds TB MFMAs (prefill-sized
+// batches read and dequantize each weight once per 16 TB tokens instead of
+// once per 16). Pass lanes: workgroup (x, e, z) takes passes z, z + Z, ...
+// of expert e (Z = gridDim.z), so the passes of a heavily routed expert run
+// side by side.
+template <int TYPE, bool F32_OUT, bool GLU, int TB>
 __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     const uint8_t* __restrict__ w, int64_t expert_stride, int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
     int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
     int64_t rows_per_wg, int glu_op, int swapped) {
-  extern __shared__ __align__(16) uint16_t As[];  // kMoeTok rows of `pitch` bf16
-  __shared__ int32_t s_pair[kMoeTok];
-  __shared__ int64_t s_xrow[kMoeTok];
+  constexpr int kPass = kMoeTok * TB;  // tokens per pass
+  extern __shared__ __align__(16) uint16_t As[];  // kPass rows of `pitch` bf16
+  __shared__ int32_t s_pair[kPass];
+  __shared__ int64_t s_xrow[kPass];
   __shared__ int32_t s_list[kFusedPairs];
   __shared__ int32_t s_n;
   constexpr int R = kStreamRing<TYPE>;
   const int64_t e = blockIdx.y;
+  const int32_t lane_z = static_cast<int32_t>(blockIdx.z), n_lanes_z = static_cast<int32_t>(gridDim.z);
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t feat = GLU ? n_rows / 2 : n_rows;  // output columns
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
   const int64_t r1 = min(r0 + rows_per_wg, feat);
   int32_t begin, end;
   const int32_t* lst;
-  moe_route<F32_OUT>(ids, n_pairs, n_expert, e, offsets, list, s_list, s_n, y, feat, r0, r1, tid, kStreamThreads,
-                     begin, end, lst);
-  if (begin >= end || r0 >= r1) return;
+  // Only pass lane 0 clears the rows of pairs routed nowhere (its columns).
+  moe_route<F32_OUT>(ids, n_pairs, n_expert, e, offsets, list, s_list, s_n, y, feat, r0, lane_z == 0 ? r1 : r0, tid,
+                     kStreamThreads, begin, end, lst);
+  if (begin + lane_z * kPass >= end || r0 >= r1) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;
@@ -1098,10 +1123,11 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   const bool ragged = k % 128 != 0;
   const auto row_of = [&](int64_t j) { return r0 + 16 * (wave + 8 * j) + (lane & 15); };
 
-  for (int32_t t0 = begin; t0 < end; t0 += kMoeTok) {
-    const int nt = min(kMoeTok, end - t0);
+  for (int32_t t0 = begin + lane_z * kPass; t0 < end; t0 += n_lanes_z * kPass) {
+    const int nt = min(kPass, end - t0);
+    const int nblk = (nt + kMoeTok - 1) / kMoeTok;  // row blocks with routed tokens
     __syncthreads();
-    if (tid < kMoeTok) {
+    if (tid < kPass) {
       const int32_t pr = tid < nt ? lst[t0 + tid] : -1;
       s_pair[tid] = pr;
       if (pr >= 0) {
@@ -1138,11 +1164,17 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     __syncthreads();
 
     // MFMA rows past nt read row nt - 1; their outputs are dropped.
-    const uint16_t* arow = As + min(lane & 15, nt - 1) * pitch + 8 * g;
-    f32x4_t acc[4];
+    const uint16_t* arow[TB];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4_t gate = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};  // GLU: the group's gate sums
+    for (int tb = 0; tb < TB; ++tb) arow[tb] = As + min(kMoeTok * tb + (lane & 15), nt - 1) * pitch + 8 * g;
+    f32x4_t acc[TB][4];
+    f32x4_t gate[TB];  // GLU: the group's gate sums
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc[tb][s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      gate[tb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     int cj = 0, cu = 0;  // compute pointer
     const auto compute = [&](int slot) {
       const int ku = cu < units ? cu : cu - static_cast<int>(units);  // unit within the row
@@ -1157,41 +1189,52 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
             if (ragged && st == steps - 1 && 32 * (4 * st + g) >= k) pc.zero();
           }
           pc.prep();
-          const uint16_t* ak = arow + 8 * 16 * st;
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             const bf16x8_t b = __builtin_bit_cast(bf16x8_t, pc.dequant(s));
-            const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ak + 8 * 4 * s);
-            acc[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[s], 0, 0, 0);
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+              if (TB == 1 || tb < nblk) {
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(arow[tb] + 8 * 16 * st + 8 * 4 * s);
+                acc[tb][s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[tb][s], 0, 0, 0);
+              }
+            }
           }
         }
       }
       ++cu;
       if (GLU && cu == units) {
-        gate = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int tb = 0; tb < TB; ++tb) {
+          gate[tb] = (acc[tb][0] + acc[tb][1]) + (acc[tb][2] + acc[tb][3]);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc[tb][s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
       } else if (cu == gunits) {
-        // acc: lane l holds rows 4 (l / 16) + i (routed pairs) of column l % 16.
+        // acc[tb]: lane l holds rows 16 tb + 4 (l / 16) + i (routed pairs) of
+        // column l % 16.
         const int64_t n = row_of(cj);
-        f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-        if constexpr (GLU) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            sum[i] = swapped ? glu_act(glu_op, sum[i]) * gate[i] : glu_act(glu_op, gate[i]) * sum[i];
-        }
+        for (int tb = 0; tb < TB; ++tb) {
+          f32x4_t sum = (acc[tb][0] + acc[tb][1]) + (acc[tb][2] + acc[tb][3]);
+          if constexpr (GLU) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int32_t pr = s_pair[4 * g + i];
-          if (pr >= 0 && n < r1) {
-            if constexpr (F32_OUT)
-              static_cast<float*>(y)[pr * feat + n] = sum[i];
-            else
-              static_cast<__bf16*>(y)[pr * feat + n] = static_cast<__bf16>(sum[i]);
+            for (int i = 0; i < 4; ++i)
+              sum[i] = swapped ? glu_act(glu_op, sum[i]) * gate[tb][i] : glu_act(glu_op, gate[tb][i]) * sum[i];
           }
-        }
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          for (int i = 0; i < 4; ++i) {
+            const int32_t pr = s_pair[kMoeTok * tb + 4 * g + i];
+            if (pr >= 0 && n < r1) {
+              if constexpr (F32_OUT)
+                static_cast<float*>(y)[pr * feat + n] = sum[i];
+              else
+                static_cast<__bf16*>(y)[pr * feat + n] = static_cast<__bf16>(sum[i]);
+            }
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc[tb][s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
         cu = 0;
         ++cj;
       }
@@ -1215,29 +1258,67 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
 }
 
 // Dynamic LDS of the streaming form for k (0 when it does not fit).
-int64_t stream_lds_bytes(int64_t k) {
+// Dynamic LDS budget of the streaming form (the rest of the CU's 160 KiB
+// holds its static arrays).
+constexpr int64_t kStreamLdsMax = 150 * 1024;
+
+// Dynamic LDS of the streaming form for k with tb row blocks per pass (0
+// when it does not fit; tb = 1 fits every k <= kStreamMaxK).
+int64_t stream_lds_bytes(int64_t k, int tb = 1) {
   if (k > kStreamMaxK) return 0;
-  return kMoeTok * (((k + 127) / 128) * 128 + kAPad) * 2;
+  const int64_t bytes = int64_t(kMoeTok) * tb * (((k + 127) / 128) * 128 + kAPad) * 2;
+  return bytes <= kStreamLdsMax ? bytes : 0;
+}
+
+// Row blocks per pass: enough for the average expert's routed tokens
+// (prefill batches), as far as the activations of k fit in LDS.
+int stream_tb(int64_t k, int64_t n_pairs, int64_t n_expert) {
+  const int64_t avg = ceil_div(n_pairs, n_expert);
+  if (avg > 2 * kMoeTok && stream_lds_bytes(k, 4) > 0) return 4;
+  if (avg > kMoeTok && stream_lds_bytes(k, 2) > 0) return 2;
+  return 1;
+}
+
+template <int TYPE, bool F32_OUT, bool GLU, int TB>
+int launch_stream_tb(const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
+                     const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
+                     const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, hipStream_t s) {
+  const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU, TB>;
+  const int64_t lds = stream_lds_bytes(k, TB);
+  const int64_t lds_max = TB == 1 ? stream_lds_bytes(kStreamMaxK) : kStreamLdsMax;
+  const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), static_cast<int>(lds_max));
+  if (rc != SPIRAL_OK) return rc;
+  // About two workgroups per CU in all, each over a contiguous range of
+  // whole 16-row groups of one expert (GLU: of its output features); pass
+  // lanes (grid z) for batches whose average expert needs several passes.
+  const int64_t feat = GLU ? n_rows / 2 : n_rows;
+  const int64_t per_expert = std::max<int64_t>(1, ceil_div(2 * device_cu_count(), n_expert));
+  const int64_t rows_per_wg = ceil_div(ceil_div(feat, per_expert), 16) * 16;
+  const int64_t lanes = std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(n_pairs, n_expert * kMoeTok * TB)));
+  const dim3 grid(static_cast<unsigned>(ceil_div(feat, rows_per_wg)), static_cast<unsigned>(n_expert),
+                  static_cast<unsigned>(lanes));
+  hipLaunchKernelGGL(kern, grid, dim3(kStreamThreads), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
+                     expert_stride, n_rows, k, x, x_slots, top_k, ids, static_cast<int32_t>(n_pairs),
+                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg, glu_op, swapped);
+  return launch_status();
 }
 
 template <int TYPE, bool F32_OUT, bool GLU>
 int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
                   const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
                   const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, hipStream_t s) {
-  const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU>;
-  const int64_t lds = stream_lds_bytes(k);
-  const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), static_cast<int>(stream_lds_bytes(kStreamMaxK)));
-  if (rc != SPIRAL_OK) return rc;
-  // About two workgroups per CU in all, each over a contiguous range of
-  // whole 16-row groups of one expert (GLU: of its output features).
-  const int64_t feat = GLU ? n_rows / 2 : n_rows;
-  const int64_t per_expert = std::max<int64_t>(1, ceil_div(2 * device_cu_count(), n_expert));
-  const int64_t rows_per_wg = ceil_div(ceil_div(feat, per_expert), 16) * 16;
-  const dim3 grid(static_cast<unsigned>(ceil_div(feat, rows_per_wg)), static_cast<unsigned>(n_expert));
-  hipLaunchKernelGGL(kern, grid, dim3(kStreamThreads), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
-                     expert_stride, n_rows, k, x, x_slots, top_k, ids, static_cast<int32_t>(n_pairs),
-                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg, glu_op, swapped);
-  return launch_status();
+  // The fused GLU form keeps TB <= 2 (four blocks of gate sums beside four
+  // of accumulators exceed the registers of two waves a SIMD).
+  const int tb = std::min(stream_tb(k, n_pairs, n_expert), GLU ? 2 : 4);
+#define SPIRAL_STREAM_TB(TBV)                                                                                      \
+  launch_stream_tb<TYPE, F32_OUT, GLU, TBV>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, \
+                                            offsets, list, y, glu_op, swapped, s)
+  if constexpr (!GLU) {
+    if (tb == 4) return SPIRAL_STREAM_TB(4);
+  }
+  if (tb == 2) return SPIRAL_STREAM_TB(2);
+  return SPIRAL_STREAM_TB(1);
+#undef SPIRAL_STREAM_TB
 }
 
 // ---- dense small-batch form (ggml MUL_MAT with 2 .. 16 rows of x) --------
