@@ -97,3 +97,25 @@ def test_prefill_glu(cuda, qtype, n_tokens):
     assert torch.equal(fused, ops.glu(prod, ops.GLU_SWIGLU))
     ref = O.glu_f64(_moe_ref(qtype, raws, 2 * F, k, ids, x), ops.GLU_SWIGLU)
     assert rel_err(fused.cpu().numpy(), ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("stage", ["gate_up", "down"])
+def test_prefill_bench_shape_equals_decode_calls(cuda, stage):
+    """The prefill workload at its own size (128 experts of 1536 x 2048 /
+    2048 x 768 Q4_0, 1024 tokens, top-8, per-slot inputs for down; passes
+    of 32 / 64 tokens): bit for bit the same as sixteen decode-sized calls
+    of 64 tokens, and sampled rows against the float64 oracle."""
+    n_expert, top_k, n_tokens = 128, 8, 1024
+    n, k, xs = (1536, 2048, 1) if stage == "gate_up" else (2048, 768, 8)
+    w, per, raws, ids, x = _moe_inputs(cuda, O.Q4_0, n_expert, n, k, n_tokens, top_k, xs, 68)
+    xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
+    big = ops.mul_mat_id(O.Q4_0, w, per, n_expert, n, k, xd, idd, out_dtype=torch.float32)
+    parts = [ops.mul_mat_id(O.Q4_0, w, per, n_expert, n, k, xd[t:t + 64].contiguous(), idd[t:t + 64].contiguous(),
+                            out_dtype=torch.float32) for t in range(0, n_tokens, 64)]
+    torch.cuda.synchronize()
+    assert torch.equal(big, torch.cat(parts))
+    sel = [(t, s) for t in range(0, n_tokens, 97) for s in (0, top_k - 1)]
+    ref = np.stack([O.matmul_f64(O.dequant(O.Q4_0, raws[ids[t, s]], n, k), x[t, s % xs][None, :])[0]
+                    for t, s in sel])
+    got = np.stack([big[t, s].cpu().numpy() for t, s in sel])
+    assert rel_err(got, ref) <= REL_TOL_EXACT_W
