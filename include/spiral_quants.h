@@ -274,6 +274,31 @@ int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride,
 int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx,
                int64_t F, int64_t rows, float* y, int64_t ldy, void* stream);
 
+/* ggml's split GLU form fused into MUL_MAT_ID: the gate and up experts are
+ * two stacks (w_gate, w_up) of n_expert planar n_ff x k matrices at the same
+ * expert_stride, as in MoE FFNs stored with separate ffn_gate_exps and
+ * ffn_up_exps tensors (ggml: two MUL_MAT_ID nodes and a GLU over both).
+ * y[t][s][f] = act(gate) * up (act(up) * gate when swapped), y
+ * [n_tokens][top_k][n_ff], the two products never stored. Same arguments,
+ * limits (spiral_mul_mat_id_glu_fits(type, 2 * n_ff, k)), workspace and
+ * errors as spiral_mul_mat_id_glu; w_up 16-byte aligned. Each output equals
+ * MUL_MAT_ID of each stack followed by spiral_glu_split, bit for bit. */
+int spiral_mul_mat_id_glu_split(int type, const void* w_gate, const void* w_up,
+                                int64_t expert_stride, int64_t n_expert,
+                                int64_t n_ff, int64_t k, const uint16_t* x,
+                                int64_t x_slots, const int32_t* ids,
+                                int64_t n_tokens, int64_t top_k, int glu_op,
+                                int swapped, void* y, int y_type,
+                                void* workspace, int64_t workspace_bytes,
+                                void* stream);
+
+/* ggml's split GLU on its own: y[r][f] = act(gate[r][f]) * up[r][f]
+ * (act(up) * gate when swapped), rows of stride ldg / ldu / ldy elements;
+ * F32 in and out, device pointers. */
+int spiral_glu_split(int glu_op, int swapped, const float* gate, int64_t ldg,
+                     const float* up, int64_t ldu, int64_t F, int64_t rows,
+                     float* y, int64_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,6 +61,9 @@ SIGNATURES = {
     "spiral_mul_mat_id_glu": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _int, _int,
                                      _p, _int, _p, _i64, _p]),
     "spiral_glu": (_int, [_int, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "spiral_mul_mat_id_glu_split": (_int, [_int, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _int,
+                                           _int, _p, _int, _p, _i64, _p]),
+    "spiral_glu_split": (_int, [_int, _int, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
 }
 
 _lib = None

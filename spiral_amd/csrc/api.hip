@@ -1,4 +1,6 @@
 // Validation and dispatch for the matrix-product entry points.
+#include <algorithm>
+
 #include "common.h"
 
 namespace spiral {
@@ -15,9 +17,11 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs);
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s);
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up = nullptr);
 int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
         hipStream_t s);
+int glu_split(int op, int swapped, const float* xg, int64_t ldg, const float* xu, int64_t ldu, int64_t n,
+              int64_t rows, float* y, int64_t ldy, hipStream_t s);
 bool moe_glu_fits_k(int64_t k);
 void* moe_static_scratch(int& rc);
 
@@ -151,6 +155,42 @@ int spiral_mul_mat_id_glu(int type, const void* w, int64_t expert_stride, int64_
   if (rc != SPIRAL_OK) return rc;
   return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, glu_op,
              swapped, workspace, static_cast<hipStream_t>(stream));
+}
+
+int spiral_mul_mat_id_glu_split(int type, const void* w_gate, const void* w_up, int64_t expert_stride,
+                                int64_t n_expert, int64_t n_ff, int64_t k, const uint16_t* x, int64_t x_slots,
+                                const int32_t* ids, int64_t n_tokens, int64_t top_k, int glu_op, int swapped, void* y,
+                                int y_type, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
+  if (n_tokens == 0 && is_quant_type(type) && (y_type == SPIRAL_TYPE_BF16 || y_type == SPIRAL_TYPE_F32))
+    return SPIRAL_OK;
+  if (w_up == nullptr) return SPIRAL_ERR_NULL;
+  int rc = check_mul_mat_id(type, w_gate, expert_stride, n_expert, n_ff, k, x, x_slots, ids, n_tokens, top_k, y,
+                            y_type, workspace, workspace_bytes);
+  if (rc != SPIRAL_OK) return rc;
+  if (!aligned16(w_up)) return SPIRAL_ERR_ALIGN;
+  if (n_ff > INT64_MAX / 2 || !spiral_mul_mat_id_glu_fits(type, 2 * n_ff, k)) return SPIRAL_ERR_SHAPE;
+  rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return moe(type, w_gate, expert_stride, n_expert, 2 * n_ff, k, x, x_slots, ids, n_tokens, top_k, y, y_type, glu_op,
+             swapped, workspace, static_cast<hipStream_t>(stream), w_up);
+}
+
+int spiral_glu_split(int glu_op, int swapped, const float* gate, int64_t ldg, const float* up, int64_t ldu, int64_t F,
+                     int64_t rows, float* y, int64_t ldy, void* stream) {
+  if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
+  int64_t span = 0;
+  const int64_t ld = std::max(ldg, std::max(ldu, ldy));
+  if (F < 0 || rows < 0 || ldg < F || ldu < F || ldy < F || __builtin_mul_overflow(rows, ld, &span))
+    return SPIRAL_ERR_SHAPE;
+  if (F == 0 || rows == 0) return SPIRAL_OK;
+  if (gate == nullptr || up == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
+  if ((reinterpret_cast<uintptr_t>(gate) & 3u) != 0 || (reinterpret_cast<uintptr_t>(up) & 3u) != 0 ||
+      (reinterpret_cast<uintptr_t>(y) & 3u) != 0)
+    return SPIRAL_ERR_ALIGN;
+  const int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return glu_split(glu_op, swapped, gate, ldg, up, ldu, F, rows, y, ldy, static_cast<hipStream_t>(stream));
 }
 
 int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx, int64_t F, int64_t rows, float* y, int64_t ldy,

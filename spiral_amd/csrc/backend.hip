@@ -335,13 +335,40 @@ int compute_mul_mat_id_glu(spiral_backend* be, const spiral_tensor* t, const spi
                                be->stream);
 }
 
-// GLU over rows of src0 (contiguous outer dimensions, checked by supports_op).
+// GLU over rows of src0, or of src0 and src1 (split form); contiguous outer
+// dimensions, checked by supports_op.
 int compute_glu(spiral_backend* be, const spiral_tensor* t) {
   const spiral_tensor* a = t->src[0];
+  const spiral_tensor* b2 = t->src[1];
   const int64_t rows = t->ne[1] * t->ne[2] * t->ne[3];
+  if (b2 != nullptr)
+    return spiral_glu_split(t->op_params[0], t->op_params[1], static_cast<const float*>(a->data),
+                            static_cast<int64_t>(a->nb[1] / 4), static_cast<const float*>(b2->data),
+                            static_cast<int64_t>(b2->nb[1] / 4), t->ne[0], rows, static_cast<float*>(t->data),
+                            static_cast<int64_t>(t->nb[1] / 4), be->stream);
   return spiral_glu(t->op_params[0], t->op_params[1], static_cast<const float*>(a->data),
                     static_cast<int64_t>(a->nb[1] / 4), t->ne[0], rows, static_cast<float*>(t->data),
                     static_cast<int64_t>(t->nb[1] / 4), be->stream);
+}
+
+// ggml's split form fused: MUL_MAT_ID over the gate experts (g->src[0]) and
+// over the up experts (g->src[1]), same activations and ids, then GLU g.
+int compute_mul_mat_id_glu_split(spiral_backend* be, const spiral_tensor* g) {
+  const spiral_tensor* tg = g->src[0];
+  const spiral_tensor* tu = g->src[1];
+  const spiral_tensor* a = tg->src[0];
+  const spiral_tensor* b = tg->src[1];
+  const spiral_tensor* ids = tg->src[2];
+  int rc;
+  int64_t ld1, ld2, ld3;
+  const uint16_t* x = act_bf16(b, be->scratch, true, be->stream, ld1, ld2, ld3, rc);
+  if (rc != SPIRAL_OK) return rc;
+  const size_t xbytes = align_up(static_cast<size_t>(b->ne[0] * b->ne[1] * b->ne[2]) * 2, kAlign);
+  const int64_t wsb = spiral_mul_mat_id_workspace_bytes(a->ne[2], ids->ne[1], ids->ne[0]);
+  return spiral_mul_mat_id_glu_split(a->type, a->data, tu->src[0]->data, static_cast<int64_t>(a->nb[2]), a->ne[2],
+                                     a->ne[1], a->ne[0], x, b->ne[1], static_cast<const int32_t*>(ids->data),
+                                     ids->ne[1], ids->ne[0], g->op_params[0], g->op_params[1], g->data,
+                                     SPIRAL_TYPE_F32, be->scratch + xbytes, wsb, be->stream);
 }
 
 // Node i (MUL_MAT_ID) can run fused with node i + 1 (GLU over it): nothing
@@ -352,7 +379,7 @@ bool fusable_glu(const spiral_cgraph* graph, int32_t i) {
   if (i + 1 >= graph->n_nodes) return false;
   const spiral_tensor* t = graph->nodes[i];
   const spiral_tensor* g = graph->nodes[i + 1];
-  if (t->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU || g->src[0] != t) return false;
+  if (t->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU || g->src[0] != t || g->src[1] != nullptr) return false;
   if ((t->flags & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || !fully_contiguous(g, 4)) return false;
   const spiral_tensor* a = t->src[0];
   if (!spiral_mul_mat_id_glu_fits(a->type, a->ne[1], a->ne[0])) return false;
@@ -360,6 +387,35 @@ bool fusable_glu(const spiral_cgraph* graph, int32_t i) {
     if (j == i + 1) continue;
     for (int s = 0; s < SPIRAL_MAX_SRC; ++s)
       if (graph->nodes[j]->src[s] == t) return false;
+  }
+  return true;
+}
+
+// Nodes i and i + 1 (MUL_MAT_ID, either order) and i + 2 (split GLU over
+// both) can run as one pass: the two products share activations and ids,
+// their expert stacks have one type, shape and stride, neither product is a
+// graph output or read by any other node, the fused pass covers the shape,
+// and the GLU output is contiguous.
+bool fusable_glu_split(const spiral_cgraph* graph, int32_t i) {
+  if (i + 2 >= graph->n_nodes) return false;
+  const spiral_tensor* t0 = graph->nodes[i];
+  const spiral_tensor* t1 = graph->nodes[i + 1];
+  const spiral_tensor* g = graph->nodes[i + 2];
+  if (t0->op != SPIRAL_OP_MUL_MAT_ID || t1->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU) return false;
+  if (g->src[1] == nullptr || !((g->src[0] == t0 && g->src[1] == t1) || (g->src[0] == t1 && g->src[1] == t0)))
+    return false;
+  if (((t0->flags | t1->flags) & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || !fully_contiguous(g, 4)) return false;
+  if (t0->src[1] != t1->src[1] || t0->src[2] != t1->src[2]) return false;
+  const spiral_tensor* a0 = t0->src[0];
+  const spiral_tensor* a1 = t1->src[0];
+  if (a0->type != a1->type || a0->nb[2] != a1->nb[2]) return false;
+  for (int d = 0; d < 3; ++d)
+    if (a0->ne[d] != a1->ne[d]) return false;
+  if (a0->ne[1] > INT64_MAX / 2 || !spiral_mul_mat_id_glu_fits(a0->type, 2 * a0->ne[1], a0->ne[0])) return false;
+  for (int32_t j = 0; j < graph->n_nodes; ++j) {
+    if (j == i + 2) continue;
+    for (int s = 0; s < SPIRAL_MAX_SRC; ++s)
+      if (graph->nodes[j]->src[s] == t0 || graph->nodes[j]->src[s] == t1) return false;
   }
   return true;
 }
@@ -590,22 +646,28 @@ int spiral_supports_op(const spiral_tensor* t) {
       return 1;
     }
     case SPIRAL_OP_GLU: {
+      // Single-tensor form (src[1] NULL: halves of src0) or split form
+      // (src0 and src1 of the output's shape).
       const spiral_tensor* a = t->src[0];
-      if (a == nullptr || t->src[1] != nullptr) return 0;
+      const spiral_tensor* b2 = t->src[1];
+      if (a == nullptr) return 0;
       const int32_t op = t->op_params[0], swapped = t->op_params[1];
       if (op != SPIRAL_GLU_REGLU && op != SPIRAL_GLU_GEGLU && op != SPIRAL_GLU_SWIGLU && op != SPIRAL_GLU_GEGLU_ERF &&
           op != SPIRAL_GLU_GEGLU_QUICK)
         return 0;
       if (swapped != 0 && swapped != 1) return 0;
-      if (a->type != SPIRAL_TYPE_F32 || t->type != SPIRAL_TYPE_F32) return 0;
-      if (!rows_contiguous(a, 4) || !rows_contiguous(t, 4)) return 0;
-      // Rows evenly strided across the outer dimensions (one row stride).
-      for (const spiral_tensor* u : {a, t})
+      for (const spiral_tensor* u : {a, b2, t}) {
+        if (u == nullptr) continue;
+        if (u->type != SPIRAL_TYPE_F32 || !rows_contiguous(u, 4)) return 0;
+        // Rows evenly strided across the outer dimensions (one row stride).
         if (u->nb[2] != u->ne[1] * u->nb[1] || u->nb[3] != u->ne[2] * u->nb[2]) return 0;
-      if (a->ne[0] != 2 * t->ne[0]) return 0;
-      for (int d = 1; d < SPIRAL_MAX_DIMS; ++d)
-        if (a->ne[d] != t->ne[d]) return 0;
-      if ((reinterpret_cast<uintptr_t>(a->data) & 3) != 0 || (reinterpret_cast<uintptr_t>(t->data) & 3) != 0) return 0;
+        if ((reinterpret_cast<uintptr_t>(u->data) & 3) != 0) return 0;
+      }
+      if (a->ne[0] != (b2 == nullptr ? 2 : 1) * t->ne[0]) return 0;
+      for (int d = 0; d < SPIRAL_MAX_DIMS; ++d) {
+        if (d > 0 && a->ne[d] != t->ne[d]) return 0;
+        if (b2 != nullptr && b2->ne[d] != t->ne[d]) return 0;
+      }
       return 1;
     }
     default:
@@ -657,6 +719,11 @@ int spiral_backend_graph_compute(spiral_backend* be, const spiral_cgraph* graph)
     if (fusable_glu(graph, i)) {
       rc = compute_mul_mat_id_glu(be, t, graph->nodes[i + 1]);
       ++i;
+      continue;
+    }
+    if (fusable_glu_split(graph, i)) {
+      rc = compute_mul_mat_id_glu_split(be, graph->nodes[i + 2]);
+      i += 2;
       continue;
     }
     switch (t->op) {

@@ -45,7 +45,9 @@
 // output features; a wave streams feature group j's gate rows and then its
 // up rows through the same register ring, keeps the gate sums, and writes
 // act(gate) * up (act(up) * gate when swapped) to a [pair][F] output, so
-// the [pair][2F] product never reaches memory.
+// the [pair][2F] product never reaches memory. ggml's split form (gate and
+// up experts in two tensors of F rows, two MUL_MAT_ID nodes and a GLU over
+// both) runs the same way with the up rows taken from the second stack.
 #include <algorithm>
 #include <mutex>
 
@@ -806,6 +808,21 @@ __global__ void __launch_bounds__(256) glu_kernel(const float* __restrict__ x, i
   }
 }
 
+// ggml's split form: gate and up rows in two tensors; y = act(gate) * up
+// (act(up) * gate when swapped).
+__global__ void __launch_bounds__(256) glu_split_kernel(const float* __restrict__ xg, int64_t ldg,
+                                                        const float* __restrict__ xu, int64_t ldu,
+                                                        float* __restrict__ y, int64_t ldy, int64_t n, int64_t rows,
+                                                        int op, int swapped) {
+  const int64_t total = n * rows;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = i / n, c = i - r * n;
+    const float g = xg[r * ldg + c], u = xu[r * ldu + c];
+    y[r * ldy + c] = swapped ? glu_act(op, u) * g : glu_act(op, g) * u;
+  }
+}
+
 // ---- streaming form (the decode path) ------------------------------------
 //
 // When the activations of 16 tokens over the whole k fit in LDS (k <= 4096)
@@ -1088,7 +1105,7 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     const uint8_t* __restrict__ w, int64_t expert_stride, int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
     int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
-    int64_t rows_per_wg, int glu_op, int swapped) {
+    int64_t rows_per_wg, int glu_op, int swapped, const uint8_t* __restrict__ w_up) {
   constexpr int kPass = kMoeTok * TB;  // tokens per pass
   extern __shared__ __align__(16) uint16_t As[];  // kPass rows of `pitch` bf16
   __shared__ int32_t s_pair[kPass];
@@ -1114,7 +1131,12 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   const int64_t nb = k / block_elems(TYPE);
   const int64_t steps = (k + 127) / 128;
   const int pitch = static_cast<int>(steps * 128 + kAPad);
-  const Planes P = make_planes<TYPE>(w + e * expert_stride, n_rows, nb);
+  // GLU split form (w_up set): gate rows in w, up rows in w_up, F rows each.
+  const bool split = GLU && w_up != nullptr;
+  const int64_t mat_rows = split ? feat : n_rows;  // rows of each expert matrix
+  const Planes P = make_planes<TYPE>(w + e * expert_stride, mat_rows, nb);
+  const Planes Pu = split ? make_planes<TYPE>(w_up + e * expert_stride, mat_rows, nb) : P;
+  const int64_t up_row0 = split ? 0 : feat;  // first up row in its matrix
   // This wave's groups: ordinals j = 0 .. my_groups - 1, group wave + 8 j.
   const int64_t groups = (r1 - r0 + 15) / 16;
   const int64_t my_groups = groups > wave ? (groups - wave + 7) / 8 : 0;
@@ -1144,16 +1166,18 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
     U ring[R];
     const int n_units = static_cast<int>(my_groups * gunits);
     int lj = 0, lu = 0, nl = 0;
-    typename U::Addr la = U::addr(row_of(0) - (lane & 15), n_rows, nb, lane);
+    typename U::Addr la = U::addr(row_of(0) - (lane & 15), mat_rows, nb, lane);
     const auto issue = [&](int slot) {
-      ring[slot].load(P, la, lu < units ? lu : lu - static_cast<int>(units), nb);
+      // Gate (or only) rows from P, up rows from Pu: a select of the buffer
+      // descriptors, so the load itself is never under a branch.
+      ring[slot].load(lu < units ? P : Pu, la, lu < units ? lu : lu - static_cast<int>(units), nb);
       if (++nl < n_units) {
         ++lu;
-        if (GLU && lu == units) la = U::addr(feat + row_of(lj) - (lane & 15), n_rows, nb, lane);  // up rows
+        if (GLU && lu == units) la = U::addr(up_row0 + row_of(lj) - (lane & 15), mat_rows, nb, lane);  // up rows
         if (lu == gunits) {
           lu = 0;
           ++lj;
-          la = U::addr(row_of(lj) - (lane & 15), n_rows, nb, lane);
+          la = U::addr(row_of(lj) - (lane & 15), mat_rows, nb, lane);
         }
       }
     };
@@ -1282,7 +1306,8 @@ int stream_tb(int64_t k, int64_t n_pairs, int64_t n_expert) {
 template <int TYPE, bool F32_OUT, bool GLU, int TB>
 int launch_stream_tb(const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
                      const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
-                     const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, hipStream_t s) {
+                     const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped,
+                     const void* w_up, hipStream_t s) {
   const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU, TB>;
   const int64_t lds = stream_lds_bytes(k, TB);
   const int64_t lds_max = TB == 1 ? stream_lds_bytes(kStreamMaxK) : kStreamLdsMax;
@@ -1299,20 +1324,22 @@ int launch_stream_tb(const void* w, int64_t expert_stride, int64_t n_expert, int
                   static_cast<unsigned>(lanes));
   hipLaunchKernelGGL(kern, grid, dim3(kStreamThreads), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
                      expert_stride, n_rows, k, x, x_slots, top_k, ids, static_cast<int32_t>(n_pairs),
-                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg, glu_op, swapped);
+                     static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg, glu_op, swapped,
+                     static_cast<const uint8_t*>(w_up));
   return launch_status();
 }
 
 template <int TYPE, bool F32_OUT, bool GLU>
 int launch_stream(const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
                   const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
-                  const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, hipStream_t s) {
+                  const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped, const void* w_up,
+                  hipStream_t s) {
   // The fused GLU form keeps TB <= 2 (four blocks of gate sums beside four
   // of accumulators exceed the registers of two waves a SIMD).
   const int tb = std::min(stream_tb(k, n_pairs, n_expert), GLU ? 2 : 4);
 #define SPIRAL_STREAM_TB(TBV)                                                                                      \
   launch_stream_tb<TYPE, F32_OUT, GLU, TBV>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, \
-                                            offsets, list, y, glu_op, swapped, s)
+                                            offsets, list, y, glu_op, swapped, w_up, s)
   if constexpr (!GLU) {
     if (tb == 4) return SPIRAL_STREAM_TB(4);
   }
@@ -1637,11 +1664,13 @@ void* moe_static_scratch(int& rc) {
 }
 
 // Arguments validated by the caller. glu_op < 0: plain MUL_MAT_ID; otherwise
-// the fused GLU form (n_rows even), which only the streaming form implements
-// (k <= kStreamMaxK, else SPIRAL_ERR_SHAPE).
+// the fused GLU form (n_rows = 2F even), which only the streaming form
+// implements (k <= kStreamMaxK, else SPIRAL_ERR_SHAPE): gate rows [0, F) and
+// up rows [F, 2F) of each expert matrix, or, with w_up set (ggml's split
+// form), the F rows of w and of w_up, both at expert_stride.
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s) {
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up) {
   const int64_t n_pairs = n_tokens * top_k;
   const int f32 = y_type == SPIRAL_TYPE_F32;
   const bool glu = glu_op >= 0;
@@ -1661,7 +1690,7 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   if (stream_lds_bytes(k) > 0) {
 #define SPIRAL_MOE_STREAM_AS(T, F, G) \
   launch_stream<T, F, G>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, offsets, list, y, \
-                         glu_op, swapped, s)
+                         glu_op, swapped, w_up, s)
 #define SPIRAL_MOE_STREAM(T)                                                                                 \
   do {                                                                                                       \
     if (glu) return f32 ? SPIRAL_MOE_STREAM_AS(T, true, true) : SPIRAL_MOE_STREAM_AS(T, false, true);        \
@@ -1710,6 +1739,17 @@ int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t row
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 8 * static_cast<int64_t>(device_cu_count()));
   hipLaunchKernelGGL(glu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, x, ldx, y, ldy, n, rows, op,
                      swapped);
+  return launch_status();
+}
+
+// Split form: gate rows at xg (stride ldg), up rows at xu (stride ldu).
+int glu_split(int op, int swapped, const float* xg, int64_t ldg, const float* xu, int64_t ldu, int64_t n,
+              int64_t rows, float* y, int64_t ldy, hipStream_t s) {
+  const int64_t total = n * rows;
+  if (total == 0) return SPIRAL_OK;
+  const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 8 * static_cast<int64_t>(device_cu_count()));
+  hipLaunchKernelGGL(glu_split_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, xg, ldg, xu, ldu, y, ldy,
+                     n, rows, op, swapped);
   return launch_status();
 }
 

@@ -168,6 +168,14 @@ def glu(a, op=GLU_SWIGLU, swapped=False, name="glu"):
     return t
 
 
+def glu_split(a, b, op=GLU_SWIGLU, swapped=False, name="glu_split"):
+    """ggml_glu_split(a, b, op) (split form): act(a) * b over equal shapes, F32."""
+    t = _node(TYPE_F32, list(a.ne), OP_GLU, [a, b], name)
+    t.op_params[0] = op
+    t.op_params[1] = int(swapped)
+    return t
+
+
 def supports_op(t):
     return bool(_lib().spiral_supports_op(ctypes.byref(t)))
 

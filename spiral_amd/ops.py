@@ -144,6 +144,43 @@ def mul_mat_id_glu(qtype, w, expert_stride, n_expert, n_rows, k, x, ids, glu_op=
     return out
 
 
+def mul_mat_id_glu_split(qtype, w_gate, w_up, expert_stride, n_expert, n_ff, k, x, ids, glu_op=GLU_SWIGLU,
+                         swapped=False, out_dtype=torch.bfloat16, workspace=None, out=None):
+    """ggml's split form in one pass: gate experts w_gate and up experts w_up
+    (n_expert planar n_ff x k matrices each, same stride); y[t, s, f] =
+    act(gate) * up (act(up) * gate when swapped), y [n_tokens, top_k, n_ff]."""
+    _require_cuda(w_gate, w_up, x, ids)
+    n_tokens, top_k = ids.shape
+    x_slots = x.shape[1]
+    ids = ids.to(torch.int32).contiguous()
+    x = x.contiguous()
+    if workspace is None:
+        workspace = mul_mat_id_workspace(n_expert, n_tokens, top_k, w_gate.device)
+    if out is None:
+        out = torch.empty((n_tokens, top_k, n_ff), dtype=out_dtype, device=w_gate.device)
+    check(lib().spiral_mul_mat_id_glu_split(qtype, _ptr(w_gate), _ptr(w_up), expert_stride, n_expert, n_ff, k,
+                                            _ptr(x), x_slots, _ptr(ids), n_tokens, top_k, glu_op, int(swapped),
+                                            _ptr(out), _out_type(out.dtype), _ptr(workspace), workspace.numel(),
+                                            _stream()), "mul_mat_id_glu_split")
+    return out
+
+
+def glu_split(gate, up, glu_op=GLU_SWIGLU, swapped=False, out=None):
+    """ggml's split GLU over float32 tensors of equal shape [..., F]:
+    act(gate) * up (act(up) * gate when swapped)."""
+    _require_cuda(gate, up)
+    if gate.dtype != torch.float32 or up.dtype != torch.float32 or gate.shape != up.shape:
+        raise TypeError("glu_split takes two float32 tensors of one shape")
+    g2 = gate.reshape(-1, gate.shape[-1]).contiguous()
+    u2 = up.reshape(-1, up.shape[-1]).contiguous()
+    F = g2.shape[1]
+    if out is None:
+        out = torch.empty(gate.shape, dtype=torch.float32, device=gate.device)
+    check(lib().spiral_glu_split(glu_op, int(swapped), _ptr(g2), F, _ptr(u2), F, F, g2.shape[0], _ptr(out), F,
+                                 _stream()), "glu_split")
+    return out
+
+
 def glu(x, glu_op=GLU_SWIGLU, swapped=False, out=None):
     """ggml GLU over the last dimension of a float32 tensor [..., 2F] -> [..., F]."""
     _require_cuda(x)
