@@ -302,6 +302,18 @@ void check_validation() {
   EXPECT(spiral_glu(SPIRAL_GLU_SWIGLU, 0, ybuf, big, big / 2 + 1, 2, ybuf, big, nullptr) != SPIRAL_OK,
          "glu overflow");
   EXPECT(spiral_glu(SPIRAL_GLU_SWIGLU, 2, ybuf, 8, 4, 2, ybuf, 4, nullptr) == SPIRAL_ERR_TYPE, "glu swapped");
+  EXPECT(spiral_glu_split(SPIRAL_GLU_SWIGLU, 0, ybuf, big, ybuf, 8, 4, big, ybuf, 8, nullptr) != SPIRAL_OK,
+         "glu_split overflow");
+  EXPECT(spiral_glu_split(SPIRAL_GLU_SWIGLU, 0, ybuf, 2, ybuf, 8, 4, 2, ybuf, 8, nullptr) == SPIRAL_ERR_SHAPE,
+         "glu_split ld");
+  EXPECT(spiral_glu_split(SPIRAL_GLU_SWIGLU, 0, nullptr, 8, ybuf, 8, 4, 2, ybuf, 8, nullptr) == SPIRAL_ERR_NULL,
+         "glu_split null");
+  EXPECT(spiral_mul_mat_id_glu_split(q, wbuf, nullptr, 144, 4, 4, 32, xbuf, 1, ids, 4, 2, SPIRAL_GLU_SWIGLU, 0, ybuf,
+                                     SPIRAL_TYPE_F32, wbuf, 4096, nullptr) == SPIRAL_ERR_NULL, "glu_split null up");
+  EXPECT(spiral_mul_mat_id_glu_split(q, wbuf, wbuf, big, 4, big / 2 + 1, 32, xbuf, 1, ids, 4, 2, SPIRAL_GLU_SWIGLU, 0,
+                                     ybuf, SPIRAL_TYPE_F32, wbuf, 4096, nullptr) != SPIRAL_OK, "glu_split at max");
+  EXPECT(spiral_mul_mat_id_glu_split(q, wbuf, wbuf + 2, 144, 4, 4, 32, xbuf, 1, ids, 4, 2, SPIRAL_GLU_SWIGLU, 0, ybuf,
+                                     SPIRAL_TYPE_F32, wbuf, 4096, nullptr) != SPIRAL_OK, "glu_split align");
   EXPECT(quants_unpack_all(q, nullptr, 64, 8, xbuf, nullptr) != SPIRAL_OK, "unpack_all null");
   EXPECT(quants_unpack_mmul_all(q, wbuf, xbuf, nullptr, 64, 8, nullptr) != SPIRAL_OK, "unpack_mmul_all null");
 
