@@ -621,17 +621,35 @@ template <int TYPE>
 __device__ __forceinline__ void moe_stage(uint16_t* As, const uint16_t* __restrict__ x, const int64_t* xrow, int nt,
                                           int64_t k, int64_t c0, int tid, int width = kMoeKC, int pitch = kMoeAPitch,
                                           int nthreads = 256) {
-  const int kItems = width / 8;
-  for (int it = tid; it < nt * kItems; it += nthreads) {
-    const int r = it / kItems, q = it % kItems;
-    const int j = q >> 4, s = (q >> 2) & 3, gg = q & 3;
-    const int64_t kb = c0 + 128 * j;
-    const uint16_t* src = x + xrow[r] + kb;
-    const int k0 = MoePiece<TYPE>::local(gg, s, 0), k4 = MoePiece<TYPE>::local(gg, s, 4);
-    uint2 lo = make_uint2(0u, 0u), hi = make_uint2(0u, 0u);
-    if (kb + k0 < k) lo = *reinterpret_cast<const uint2*>(src + k0);
-    if (kb + k4 < k) hi = *reinterpret_cast<const uint2*>(src + k4);
-    *reinterpret_cast<uint4*>(&As[r * pitch + 8 * q]) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  // Items go to threads kStageBatch at a time, every load of a batch issued
+  // before any is stored, so a thread waits once per batch for the gathered
+  // rows instead of once per item.
+  constexpr int kStageBatch = 4;
+  const int kItems = width / 8, total = nt * kItems;
+  for (int it0 = tid; it0 < total; it0 += kStageBatch * nthreads) {
+    uint2 lo[kStageBatch], hi[kStageBatch];
+#pragma unroll
+    for (int b = 0; b < kStageBatch; ++b) {
+      const int it = it0 + b * nthreads;
+      lo[b] = hi[b] = make_uint2(0u, 0u);
+      if (it < total) {
+        const int r = it / kItems, q = it % kItems;
+        const int j = q >> 4, s = (q >> 2) & 3, gg = q & 3;
+        const int64_t kb = c0 + 128 * j;
+        const uint16_t* src = x + xrow[r] + kb;
+        const int k0 = MoePiece<TYPE>::local(gg, s, 0), k4 = MoePiece<TYPE>::local(gg, s, 4);
+        if (kb + k0 < k) lo[b] = *reinterpret_cast<const uint2*>(src + k0);
+        if (kb + k4 < k) hi[b] = *reinterpret_cast<const uint2*>(src + k4);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < kStageBatch; ++b) {
+      const int it = it0 + b * nthreads;
+      if (it < total) {
+        const int r = it / kItems, q = it % kItems;
+        *reinterpret_cast<uint4*>(&As[r * pitch + 8 * q]) = make_uint4(lo[b].x, lo[b].y, hi[b].x, hi[b].y);
+      }
+    }
   }
 }
 
@@ -833,7 +851,13 @@ __global__ void __launch_bounds__(256) glu_split_kernel(const float* __restrict_
 // loads. A few workgroups per expert (about two per CU in total) each cover a
 // contiguous range of rows, so the routing scan and the activation staging
 // are paid a few hundred times per call instead of once per 64 rows.
-constexpr int kStreamThreads = 512;  // 8 waves
+// Waves per workgroup of the streaming form. Prefill passes (TB >= 2) stage
+// up to 128 KiB of activations, so one workgroup fits a CU: 12 waves (three
+// a SIMD, as their registers allow) share that staging instead of 8. The
+// fused GLU form and Q6_K at four row blocks need more registers than three
+// waves a SIMD leave them.
+template <int TYPE, bool GLU, int TB>
+constexpr int kStreamWaves = (TB >= 2 && !GLU && !(TYPE == SPIRAL_TYPE_Q6_K && TB == 4)) ? 12 : 8;
 constexpr int64_t kStreamMaxK = 4096;
 
 // Ring slots (units) in flight per wave.
@@ -1100,8 +1124,8 @@ __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32
 // once per 16). Pass lanes: workgroup (x, e, z) takes passes z, z + Z, ...
 // of expert e (Z = gridDim.z), so the passes of a heavily routed expert run
 // side by side.
-template <int TYPE, bool F32_OUT, bool GLU, int TB>
-__global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
+template <int TYPE, bool F32_OUT, bool GLU, int TB, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) moe_stream_kernel(
     const uint8_t* __restrict__ w, int64_t expert_stride, int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
     int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
@@ -1123,7 +1147,7 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   const int32_t* lst;
   // Only pass lane 0 clears the rows of pairs routed nowhere (its columns).
   moe_route<F32_OUT>(ids, n_pairs, n_expert, e, offsets, list, s_list, s_n, y, feat, r0, lane_z == 0 ? r1 : r0, tid,
-                     kStreamThreads, begin, end, lst);
+                     64 * WAVES, begin, end, lst);
   if (begin + lane_z * kPass >= end || r0 >= r1) return;
 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1137,13 +1161,13 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
   const Planes P = make_planes<TYPE>(w + e * expert_stride, mat_rows, nb);
   const Planes Pu = split ? make_planes<TYPE>(w_up + e * expert_stride, mat_rows, nb) : P;
   const int64_t up_row0 = split ? 0 : feat;  // first up row in its matrix
-  // This wave's groups: ordinals j = 0 .. my_groups - 1, group wave + 8 j.
+  // This wave's groups: ordinals j = 0 .. my_groups - 1, group wave + WAVES j.
   const int64_t groups = (r1 - r0 + 15) / 16;
-  const int64_t my_groups = groups > wave ? (groups - wave + 7) / 8 : 0;
+  const int64_t my_groups = groups > wave ? (groups - wave + WAVES - 1) / WAVES : 0;
   const int64_t units = (steps + Unit<TYPE>::kSteps - 1) / Unit<TYPE>::kSteps;
   const int64_t gunits = GLU ? 2 * units : units;  // units per group: gate, then up
   const bool ragged = k % 128 != 0;
-  const auto row_of = [&](int64_t j) { return r0 + 16 * (wave + 8 * j) + (lane & 15); };
+  const auto row_of = [&](int64_t j) { return r0 + 16 * (wave + WAVES * j) + (lane & 15); };
 
   for (int32_t t0 = begin + lane_z * kPass; t0 < end; t0 += n_lanes_z * kPass) {
     const int nt = min(kPass, end - t0);
@@ -1184,7 +1208,7 @@ __global__ void __launch_bounds__(kStreamThreads) moe_stream_kernel(
 #pragma unroll
     for (int i = 0; i < R - 1; ++i) issue(i);
     __syncthreads();
-    moe_stage<TYPE>(As, x, s_xrow, nt, k, 0, tid, static_cast<int>(steps * 128), pitch, kStreamThreads);
+    moe_stage<TYPE>(As, x, s_xrow, nt, k, 0, tid, static_cast<int>(steps * 128), pitch, 64 * WAVES);
     __syncthreads();
 
     // MFMA rows past nt read row nt - 1; their outputs are dropped.
@@ -1308,21 +1332,30 @@ int launch_stream_tb(const void* w, int64_t expert_stride, int64_t n_expert, int
                      const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_pairs, int64_t top_k,
                      const int32_t* offsets, const int32_t* list, void* y, int glu_op, int swapped,
                      const void* w_up, hipStream_t s) {
-  const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU, TB>;
+  constexpr int kWaves = kStreamWaves<TYPE, GLU, TB>;
+  const auto kern = moe_stream_kernel<TYPE, F32_OUT, GLU, TB, kWaves>;
   const int64_t lds = stream_lds_bytes(k, TB);
   const int64_t lds_max = TB == 1 ? stream_lds_bytes(kStreamMaxK) : kStreamLdsMax;
   const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), static_cast<int>(lds_max));
   if (rc != SPIRAL_OK) return rc;
-  // About two workgroups per CU in all, each over a contiguous range of
-  // whole 16-row groups of one expert (GLU: of its output features); pass
-  // lanes (grid z) for batches whose average expert needs several passes.
+  // Workgroups over contiguous ranges of whole 16-row groups of one expert
+  // (GLU: of its output features), and pass lanes (grid z) for batches whose
+  // average expert needs several passes. As many workgroups as the CUs hold
+  // at once (at most two a CU), so each pass's activations are staged once
+  // per CU; twice that with pass lanes, whose pass counts differ by one
+  // between lanes of an expert, so that the dispatcher evens them out
+  // (1024 tokens, top-8 over 128 experts, Q4_0 1536 x 2048: 203 us against
+  // 246 us for one round and 218 us for four).
   const int64_t feat = GLU ? n_rows / 2 : n_rows;
-  const int64_t per_expert = std::max<int64_t>(1, ceil_div(2 * device_cu_count(), n_expert));
-  const int64_t rows_per_wg = ceil_div(ceil_div(feat, per_expert), 16) * 16;
   const int64_t lanes = std::min<int64_t>(8, std::max<int64_t>(1, ceil_div(n_pairs, n_expert * kMoeTok * TB)));
+  const int64_t resident = static_cast<int64_t>(device_cu_count()) *
+                           std::min(2, blocks_per_cu(reinterpret_cast<const void*>(kern), 64 * kWaves, lds));
+  const int64_t rounds = lanes > 1 ? 2 : 1;
+  const int64_t per_expert = std::max<int64_t>(1, ceil_div(rounds * resident, n_expert * lanes));
+  const int64_t rows_per_wg = ceil_div(ceil_div(feat, per_expert), 16) * 16;
   const dim3 grid(static_cast<unsigned>(ceil_div(feat, rows_per_wg)), static_cast<unsigned>(n_expert),
                   static_cast<unsigned>(lanes));
-  hipLaunchKernelGGL(kern, grid, dim3(kStreamThreads), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
+  hipLaunchKernelGGL(kern, grid, dim3(64 * kWaves), static_cast<size_t>(lds), s, static_cast<const uint8_t*>(w),
                      expert_stride, n_rows, k, x, x_slots, top_k, ids, static_cast<int32_t>(n_pairs),
                      static_cast<int32_t>(n_expert), offsets, list, y, rows_per_wg, glu_op, swapped,
                      static_cast<const uint8_t*>(w_up));
