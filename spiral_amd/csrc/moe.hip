@@ -982,9 +982,9 @@ struct PieceAddr<SPIRAL_TYPE_IQ4_XS> {
 // as whole 128-byte lines (two instructions, rows 0..7 and 8..15) and moved
 // into MFMA position with ds_bpermute; loading the pieces directly would
 // fetch every line as two 64-byte halves, which the L1's miss capacity turns
-// into the limit. Lanes hold the blocks of step h of the pair in lanes
-// 32 h .. 32 h + 31, so the 32 source lanes of each permute are consecutive
-// and fall in distinct LDS banks.
+// into the limit. After arrange(), one register holds step h of the pair
+// for all 16 rows, and each permute reads every one of its 64 source lanes
+// once.
 // Other types: one k step's pieces, loaded directly.
 template <int TYPE>
 struct Unit {
@@ -999,15 +999,17 @@ struct Unit {
     return a;
   }
   __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t) { a.pa.load(pc, P, u); }
+  __device__ __forceinline__ void arrange() {}
   __device__ __forceinline__ void piece(MoePiece<TYPE>& out, int, int) const { out = pc; }
 };
 
 template <>
 struct Unit<SPIRAL_TYPE_Q4_0> {
   static constexpr int kSteps = 2;
-  // Lane l = 32 h + 4 r' + c': qa / qb hold rows r' and 8 + r' of the
-  // group, block 8 u + 4 h + c'. Lane l = 32 h + 2 r + p: dl / dh hold the
-  // dwords around d of blocks 8 u + 4 h + 2 p and + 1 of row r.
+  // As loaded, lane l = 32 h + 4 r' + c': qa / qb hold rows r' and 8 + r'
+  // of the group, block 8 u + 4 h + c' (arrange() regroups them by step).
+  // Lane l = 32 h + 2 r + p: dl / dh hold the dwords around d of blocks
+  // 8 u + 4 h + 2 p and + 1 of row r.
   uint4 qa, qb;
   uint32_t dl, dh;
   int32_t dinfo;  // 4 (first of the two blocks - nb) + byte offset of its d in dl
@@ -1047,18 +1049,31 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
     const int32_t past = dinfo >> 2;  // first block - nb
     return past >= 0 ? 0u : past == -1 ? pair & 0xffffu : pair;
   }
-  // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16).
-  __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
-    const int r = lane & 15, g = lane >> 4, b = 4 * h + g;
-    const int src = (32 * h + 4 * (r & 7) + g) << 2;
-    const uint32_t va[4] = {qa.x, qa.y, qa.z, qa.w}, vb[4] = {qb.x, qb.y, qb.z, qb.w};
-    uint32_t q[4];
+  // Once the unit's loads have arrived: qa <- step 0 of all 16 rows (rows
+  // 0..7 in lanes 0..31, rows 8..15 in lanes 32..63), qb <- step 1. One
+  // v_permlane32_swap a dword moves the upper half of qa and the lower half
+  // of qb across, so each step's pieces then come from one register.
+  __device__ __forceinline__ void arrange() {
+    uint32_t a[4] = {qa.x, qa.y, qa.z, qa.w}, b[4] = {qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t x0 = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(va[j])));
-      const uint32_t x1 = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(vb[j])));
-      q[j] = (r & 8) ? x1 : x0;
+      const auto r = __builtin_amdgcn_permlane32_swap(a[j], b[j], false, false);
+      a[j] = r[0];
+      b[j] = r[1];
     }
+    qa = make_uint4(a[0], a[1], a[2], a[3]);
+    qb = make_uint4(b[0], b[1], b[2], b[3]);
+  }
+  // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16)
+  // (after arrange()).
+  __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
+    const int r = lane & 15, g = lane >> 4, b = 4 * h + g;
+    const int src = (32 * (r >> 3) + 4 * (r & 7) + g) << 2;
+    const uint4 v = h ? qb : qa;
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(vv[j])));
     out.q = make_uint4(q[0], q[1], q[2], q[3]);
     const uint32_t dv =
         static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((32 * h + 2 * r + (g >> 1)) << 2, static_cast<int>(d_pair())));
@@ -1153,8 +1168,10 @@ __global__ void __launch_bounds__(64 * WAVES) moe_stream_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4;
   const int64_t nb = k / block_elems(TYPE);
-  const int64_t steps = (k + 127) / 128;
-  const int pitch = static_cast<int>(steps * 128 + kAPad);
+  // 32-bit counters: the loop's tests stay scalar compares (64-bit ones are
+  // VALU work on this GPU).
+  const int steps = static_cast<int>((k + 127) / 128);
+  const int pitch = steps * 128 + kAPad;
   // GLU split form (w_up set): gate rows in w, up rows in w_up, F rows each.
   const bool split = GLU && w_up != nullptr;
   const int64_t mat_rows = split ? feat : n_rows;  // rows of each expert matrix
@@ -1164,8 +1181,8 @@ __global__ void __launch_bounds__(64 * WAVES) moe_stream_kernel(
   // This wave's groups: ordinals j = 0 .. my_groups - 1, group wave + WAVES j.
   const int64_t groups = (r1 - r0 + 15) / 16;
   const int64_t my_groups = groups > wave ? (groups - wave + WAVES - 1) / WAVES : 0;
-  const int64_t units = (steps + Unit<TYPE>::kSteps - 1) / Unit<TYPE>::kSteps;
-  const int64_t gunits = GLU ? 2 * units : units;  // units per group: gate, then up
+  const int units = (steps + Unit<TYPE>::kSteps - 1) / Unit<TYPE>::kSteps;
+  const int gunits = GLU ? 2 * units : units;  // units per group: gate, then up
   const bool ragged = k % 128 != 0;
   const auto row_of = [&](int64_t j) { return r0 + 16 * (wave + WAVES * j) + (lane & 15); };
 
@@ -1225,10 +1242,11 @@ __global__ void __launch_bounds__(64 * WAVES) moe_stream_kernel(
     }
     int cj = 0, cu = 0;  // compute pointer
     const auto compute = [&](int slot) {
-      const int ku = cu < units ? cu : cu - static_cast<int>(units);  // unit within the row
+      const int ku = cu < units ? cu : cu - units;  // unit within the row
+      ring[slot].arrange();
 #pragma unroll
       for (int h = 0; h < U::kSteps; ++h) {
-        const int64_t st = static_cast<int64_t>(ku) * U::kSteps + h;
+        const int st = ku * U::kSteps + h;
         if (U::kSteps == 1 || st < steps) {
           MoePiece<TYPE> pc;
           ring[slot].piece(pc, h, lane);
@@ -1435,8 +1453,8 @@ __global__ void __launch_bounds__(kSkinnyThreads) skinny_kernel(const uint8_t* _
     return ((static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(gridDim.x) * i) * per_block + gslot) * 16;
   };
   const int64_t nb = k / block_elems(TYPE);
-  const int64_t steps = (k + 127) / 128;
-  const int units = static_cast<int>((steps + U::kSteps - 1) / U::kSteps);
+  const int steps = static_cast<int>((k + 127) / 128);
+  const int units = (steps + U::kSteps - 1) / U::kSteps;
   const Planes P = make_planes<TYPE>(w, n_rows, nb);
   // y as a buffer of (m - 1) ldy + n_rows elements (below 2^31 bytes)
   const __amdgpu_buffer_rsrc_t Y = buffer_rsrc(y, static_cast<uint32_t>(((m - 1) * ldy + n_rows) * kEsize));
@@ -1530,9 +1548,10 @@ __global__ void __launch_bounds__(kSkinnyThreads) skinny_kernel(const uint8_t* _
     ++cb;
   };
   const auto compute = [&](int slot) {
+    ring[slot].arrange();
 #pragma unroll
     for (int h = 0; h < U::kSteps; ++h) {
-      const int64_t st = static_cast<int64_t>(cu) * U::kSteps + h;
+      const int st = cu * U::kSteps + h;
       if (U::kSteps == 1 || st < steps) {
         MoePiece<TYPE> pc;
         ring[slot].piece(pc, h, lane);
