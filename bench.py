@@ -152,10 +152,10 @@ TRAFFIC_KERNELS = {
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
-    "moe_q4_0": (["moe_stream_kernel<2,false,false,1>"], None),
-    "moe_gate_up_swiglu_q4_0": (["moe_stream_kernel<2,false,true,1>"], None),
+    "moe_q4_0": (["moe_stream_kernel<2,false,false,1,8>"], None),
+    "moe_gate_up_swiglu_q4_0": (["moe_stream_kernel<2,false,true,1,8>"], None),
     # prefill: gate_up in passes of 32 tokens, down in passes of 64
-    "moe_prefill_q4_0": (["moe_stream_kernel<2,false,false,2>", "moe_stream_kernel<2,false,false,4>"], None),
+    "moe_prefill_q4_0": (["moe_stream_kernel<2,false,false,2,12>", "moe_stream_kernel<2,false,false,4,12>"], None),
 }
 
 
