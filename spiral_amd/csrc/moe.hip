@@ -82,14 +82,35 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
   __shared__ int32_t s_nbad;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kPer = kRouteChunk / kRouteThreads;
+  // Each pass over the ids takes kRouteBatch of them per thread at a time,
+  // every load issued before any is used: one load latency per batch
+  // instead of one per id.
+  constexpr int kRouteBatch = 8;
+  if (tid == 0) s_nbad = 0;
   int32_t base = 0;
   for (int32_t e0 = 0; e0 < n_expert; e0 += kRouteChunk) {
     const int32_t ne = min(kRouteChunk, n_expert - e0);
     for (int i = tid; i < kRouteChunk; i += kRouteThreads) s_cnt[i] = 0;
     __syncthreads();
-    for (int32_t p = tid; p < n_pairs; p += kRouteThreads) {
-      const int32_t e = ids[p] - e0;
-      if (e >= 0 && e < ne) atomicAdd(&s_cnt[e], 1);
+    // Count. The first chunk also collects the pairs routed nowhere (up to
+    // kRouteThreads of them; s_nbad keeps counting past that).
+    for (int32_t p0 = tid; p0 < n_pairs; p0 += kRouteBatch * kRouteThreads) {
+      int32_t id[kRouteBatch];
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        const int32_t p = p0 + u * kRouteThreads;
+        id[u] = p < n_pairs ? ids[p] : 0;
+      }
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        const int32_t p = p0 + u * kRouteThreads;
+        if (p >= n_pairs) break;
+        if (id[u] >= e0 && id[u] < e0 + ne) atomicAdd(&s_cnt[id[u] - e0], 1);
+        if (e0 == 0 && (id[u] < 0 || id[u] >= n_expert)) {
+          const int32_t b = atomicAdd(&s_nbad, 1);
+          if (b < kRouteThreads) s_bad[b] = p;
+        }
+      }
     }
     __syncthreads();
     // Exclusive scan: thread t owns experts [kPer t, kPer t + kPer).
@@ -122,17 +143,42 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
       pos += c[i];
     }
     __syncthreads();
-    for (int32_t p = tid; p < n_pairs; p += kRouteThreads) {
-      const int32_t e = ids[p] - e0;
-      if (e >= 0 && e < ne) list[atomicAdd(&s_cnt[e], 1)] = p;
+    // Scatter each pair's index into its expert's list.
+    for (int32_t p0 = tid; p0 < n_pairs; p0 += kRouteBatch * kRouteThreads) {
+      int32_t id[kRouteBatch];
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        const int32_t p = p0 + u * kRouteThreads;
+        id[u] = p < n_pairs ? ids[p] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < kRouteBatch; ++u) {
+        const int32_t p = p0 + u * kRouteThreads;
+        if (p >= n_pairs) break;
+        if (id[u] >= e0 && id[u] < e0 + ne) list[atomicAdd(&s_cnt[id[u] - e0], 1)] = p;
+      }
     }
     base += total;
     __syncthreads();
   }
   if (tid == 0) offsets[n_expert] = base;
-  // Pairs routed nowhere produce a zero row: collect them kRouteThreads at a
-  // time, then clear their rows with the whole workgroup.
+  // Pairs routed nowhere produce a zero row, cleared by the whole workgroup.
+  const auto clear_row = [&](int64_t row) {
+    for (int64_t col = tid; col < out_cols; col += kRouteThreads) {
+      if (y_f32)
+        static_cast<float*>(y)[row * out_cols + col] = 0.0f;
+      else
+        static_cast<uint16_t*>(y)[row * out_cols + col] = 0;
+    }
+  };
+  const int32_t nbad = s_nbad;  // final: the chunk loop (n_expert >= 1) ended with a barrier
+  if (nbad <= kRouteThreads) {
+    for (int32_t b = 0; b < nbad; ++b) clear_row(s_bad[b]);
+    return;
+  }
+  // More than kRouteThreads of them: collect and clear kRouteThreads at a time.
   for (int32_t p0 = 0; p0 < n_pairs; p0 += kRouteThreads) {
+    __syncthreads();
     if (tid == 0) s_nbad = 0;
     __syncthreads();
     const int32_t p = p0 + tid;
@@ -141,17 +187,8 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
       if (e < 0 || e >= n_expert) s_bad[atomicAdd(&s_nbad, 1)] = p;
     }
     __syncthreads();
-    const int32_t nbad = s_nbad;
-    for (int32_t b = 0; b < nbad; ++b) {
-      const int64_t row = s_bad[b];
-      for (int64_t col = tid; col < out_cols; col += kRouteThreads) {
-        if (y_f32)
-          static_cast<float*>(y)[row * out_cols + col] = 0.0f;
-        else
-          static_cast<uint16_t*>(y)[row * out_cols + col] = 0;
-      }
-    }
-    __syncthreads();
+    const int32_t nb = s_nbad;
+    for (int32_t b = 0; b < nb; ++b) clear_row(s_bad[b]);
   }
 }
 

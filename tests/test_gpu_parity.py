@@ -364,6 +364,28 @@ def test_moe_large_batch_routing_and_bad_ids(cuda):
     assert not out.cpu().numpy().any()
 
 
+def test_moe_route_kernel_many_ids_routed_nowhere(cuda):
+    """3000 pairs of which 1300 are routed nowhere (more than the route
+    kernel collects in one go, so it clears their rows in rounds), including
+    the extreme ids INT32_MIN and INT32_MAX; the routed pairs still match the
+    float64 oracle and the rest are zero rows over a prefilled output."""
+    n_expert, n, k, n_tokens, top_k = 8, 48, 256, 1500, 2
+    rng = np.random.default_rng(71)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    bad = rng.choice(n_tokens * top_k, 1300, replace=False)
+    flat = ids.reshape(-1)
+    flat[bad] = rng.choice(np.array([-1, n_expert, 1000, np.iinfo(np.int32).min, np.iinfo(np.int32).max],
+                                    dtype=np.int32), bad.size)
+    w, per, raws, ids, x = _moe_inputs(cuda, O.Q4_0, n_expert, n, k, n_tokens, top_k, 1, 72, ids)
+    out = torch.full((n_tokens, top_k, n), 7.0, device=cuda)
+    ops.mul_mat_id(O.Q4_0, w, per, n_expert, n, k, dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda), out=out)
+    torch.cuda.synchronize()
+    y = out.cpu().numpy()
+    nowhere = (ids < 0) | (ids >= n_expert)
+    assert nowhere.sum() == 1300 and not y[nowhere].any()
+    check_moe(y, _moe_ref(O.Q4_0, raws, n, k, ids, x), True)
+
+
 def test_moe_128_experts_gate_up(cuda):
     """The MoE workload's gate_up stage: 128 experts of 1536 x 2048 Q4_0,
     64 tokens, top-8 distinct experts per token."""
