@@ -61,7 +61,8 @@ typedef enum spiral_op {
   SPIRAL_OP_RESHAPE = 5,
   SPIRAL_OP_PERMUTE = 6,
   SPIRAL_OP_TRANSPOSE = 7,
-  SPIRAL_OP_GLU = 8 /* op_params[0]: SPIRAL_GLU_* variant, op_params[1]: swapped */
+  SPIRAL_OP_GLU = 8 /* op_params[0]: SPIRAL_GLU_* variant, op_params[1]: swapped;
+                      SWIGLU_OAI: op_params[2] alpha, [3] limit (floats) */
 } spiral_op;
 
 typedef struct spiral_buffer spiral_buffer;   /* device memory block (opaque) */
@@ -149,10 +150,12 @@ int spiral_buffer_clear(spiral_buffer* buf, uint8_t value);
  *   MUL_MAT_ID  src0 quantized [k, n, n_expert], src1 F32/BF16
  *               [k, x_slots (1 or top_k), n_tokens], src2 I32 [top_k,
  *               n_tokens], dst F32 [n, top_k, n_tokens], all contiguous;
- *   GLU         src0 F32 [2F, ...] with contiguous rows and no src1 (the
- *               single-tensor form), dst F32 [F, ...] of the same outer
- *               shape; op_params[0] REGLU / GEGLU / SWIGLU / GEGLU_ERF /
- *               GEGLU_QUICK, op_params[1] 0 or 1;
+ *   GLU         dst F32 [F, ...]; src0 F32 [2F, ...] and no src1 (the
+ *               single-tensor form), or src0 and src1 F32 [F, ...] (the
+ *               split form), all of one outer shape with contiguous, evenly
+ *               strided rows; op_params[0] REGLU / GEGLU / SWIGLU /
+ *               SWIGLU_OAI (alpha and limit as floats in op_params[2] and
+ *               [3]) / GEGLU_ERF / GEGLU_QUICK, op_params[1] 0 or 1;
  *   NONE, VIEW, RESHAPE, PERMUTE, TRANSPOSE.
  * Row lengths must be multiples of the type's block (32, Q6_K 256). */
 int spiral_supports_op(const spiral_tensor* op);

@@ -299,6 +299,23 @@ int spiral_glu_split(int glu_op, int swapped, const float* gate, int64_t ldg,
                      const float* up, int64_t ldu, int64_t F, int64_t rows,
                      float* y, int64_t ldy, void* stream);
 
+/* SPIRAL_GLU_SWIGLU_OAI (ggml's swiglu_oai, the gpt-oss FFN), which takes two
+ * parameters (ggml op_params 2 and 3) and so has entry points of its own;
+ * spiral_glu and spiral_glu_split answer SPIRAL_ERR_TYPE for it. With a the
+ * activated half and b the other (halves as in spiral_glu, swapped likewise):
+ *   x = min(a, limit), y = clamp(b, -limit, limit),
+ *   out = x / (1 + exp(-alpha x)) * (y + 1).
+ * Merged rows of 2F floats (as spiral_glu) or split gate / up rows (as
+ * spiral_glu_split); same arguments, checks and errors otherwise. No
+ * counterpart in the reference (ggml's GLU surface, README.md:11-14). */
+int spiral_glu_swiglu_oai(int swapped, float alpha, float limit,
+                          const float* x, int64_t ldx, int64_t F, int64_t rows,
+                          float* y, int64_t ldy, void* stream);
+int spiral_glu_split_swiglu_oai(int swapped, float alpha, float limit,
+                                const float* gate, int64_t ldg, const float* up,
+                                int64_t ldu, int64_t F, int64_t rows, float* y,
+                                int64_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

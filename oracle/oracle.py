@@ -198,10 +198,10 @@ def matmul_f64_exact(w_f64, x_bf16):
 
 
 # ggml GLU variants (ggml_glu_op numbering), used by the fused MUL_MAT_ID + GLU.
-GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = 0, 1, 2, 4, 5
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = 0, 1, 2, 3, 4, 5
 
 
-def glu_f64(h, op, swapped=False):
+def glu_f64(h, op, swapped=False, alpha=None, limit=None):
     """ggml's GLU over the last axis of h (..., 2F) in float64: act(a) * b with
     (a, b) the first and second halves of each row, (b, a) when swapped.
 
@@ -210,6 +210,8 @@ def glu_f64(h, op, swapped=False):
     ggml's GLU ops: REGLU relu; GEGLU gelu in its tanh form
     0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); SWIGLU silu x / (1 + e^-x);
     GEGLU_ERF 0.5 x (1 + erf(x / sqrt(2))); GEGLU_QUICK x / (1 + e^(-1.702 x)).
+    SWIGLU_OAI (gpt-oss's FFN; alpha and limit given) combines both halves:
+    x = min(a, limit), y = clip(b, -limit, limit), x / (1 + e^(-alpha x)) * (y + 1).
     """
     from scipy.special import erf
 
@@ -228,6 +230,10 @@ def glu_f64(h, op, swapped=False):
         act = 0.5 * a * (1.0 + erf(a / np.sqrt(2.0)))
     elif op == GLU_GEGLU_QUICK:
         act = a / (1.0 + np.exp(-1.702 * a))
+    elif op == GLU_SWIGLU_OAI:
+        x = np.minimum(a, limit)
+        y = np.clip(b, -limit, limit)
+        return x / (1.0 + np.exp(-alpha * x)) * (y + 1.0)
     else:
         raise ValueError(f"GLU op {op}")
     return act * b

@@ -26,7 +26,7 @@ class SpiralError(RuntimeError):
         super().__init__(f"{what}: {STATUS.get(status, status)}")
 
 
-_i64, _int, _p = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p
+_i64, _int, _p, _f32 = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -64,6 +64,8 @@ SIGNATURES = {
     "spiral_mul_mat_id_glu_split": (_int, [_int, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _int,
                                            _int, _p, _int, _p, _i64, _p]),
     "spiral_glu_split": (_int, [_int, _int, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "spiral_glu_swiglu_oai": (_int, [_int, _f32, _f32, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "spiral_glu_split_swiglu_oai": (_int, [_int, _f32, _f32, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _p]),
 }
 
 _lib = None

@@ -19,9 +19,9 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
         int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up = nullptr);
 int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
-        hipStream_t s);
+        hipStream_t s, float alpha, float limit);
 int glu_split(int op, int swapped, const float* xg, int64_t ldg, const float* xu, int64_t ldu, int64_t n,
-              int64_t rows, float* y, int64_t ldy, hipStream_t s);
+              int64_t rows, float* y, int64_t ldy, hipStream_t s, float alpha, float limit);
 bool moe_glu_fits_k(int64_t k);
 void* moe_static_scratch(int& rc);
 
@@ -176,9 +176,15 @@ int spiral_mul_mat_id_glu_split(int type, const void* w_gate, const void* w_up, 
              swapped, workspace, static_cast<hipStream_t>(stream), w_up);
 }
 
-int spiral_glu_split(int glu_op, int swapped, const float* gate, int64_t ldg, const float* up, int64_t ldu, int64_t F,
-                     int64_t rows, float* y, int64_t ldy, void* stream) {
-  if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
+}  // extern "C"
+
+namespace {
+
+// Argument checks and launch shared by the GLU entry points (alpha and limit
+// are read by SWIGLU_OAI only).
+int glu_split_entry(int glu_op, int swapped, float alpha, float limit, const float* gate, int64_t ldg,
+                    const float* up, int64_t ldu, int64_t F, int64_t rows, float* y, int64_t ldy, void* stream) {
+  if (swapped != 0 && swapped != 1) return SPIRAL_ERR_TYPE;
   int64_t span = 0;
   const int64_t ld = std::max(ldg, std::max(ldu, ldy));
   if (F < 0 || rows < 0 || ldg < F || ldu < F || ldy < F || __builtin_mul_overflow(rows, ld, &span))
@@ -190,12 +196,13 @@ int spiral_glu_split(int glu_op, int swapped, const float* gate, int64_t ldg, co
     return SPIRAL_ERR_ALIGN;
   const int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
-  return glu_split(glu_op, swapped, gate, ldg, up, ldu, F, rows, y, ldy, static_cast<hipStream_t>(stream));
+  return glu_split(glu_op, swapped, gate, ldg, up, ldu, F, rows, y, ldy, static_cast<hipStream_t>(stream), alpha,
+                   limit);
 }
 
-int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx, int64_t F, int64_t rows, float* y, int64_t ldy,
-               void* stream) {
-  if (!glu_op_ok(glu_op) || (swapped != 0 && swapped != 1)) return SPIRAL_ERR_TYPE;
+int glu_entry(int glu_op, int swapped, float alpha, float limit, const float* x, int64_t ldx, int64_t F, int64_t rows,
+              float* y, int64_t ldy, void* stream) {
+  if (swapped != 0 && swapped != 1) return SPIRAL_ERR_TYPE;
   int64_t span = 0;
   if (F < 0 || rows < 0 || F > INT64_MAX / 2 || ldx < 2 * F || ldy < F ||
       __builtin_mul_overflow(rows, ldx > ldy ? ldx : ldy, &span))
@@ -206,7 +213,34 @@ int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx, int64_t F, 
     return SPIRAL_ERR_ALIGN;
   const int rc = require_device();
   if (rc != SPIRAL_OK) return rc;
-  return glu(glu_op, swapped, x, ldx, F, rows, y, ldy, static_cast<hipStream_t>(stream));
+  return glu(glu_op, swapped, x, ldx, F, rows, y, ldy, static_cast<hipStream_t>(stream), alpha, limit);
+}
+
+}  // namespace
+
+extern "C" {
+
+int spiral_glu_split(int glu_op, int swapped, const float* gate, int64_t ldg, const float* up, int64_t ldu, int64_t F,
+                     int64_t rows, float* y, int64_t ldy, void* stream) {
+  if (!glu_op_ok(glu_op)) return SPIRAL_ERR_TYPE;
+  return glu_split_entry(glu_op, swapped, 0.0f, 0.0f, gate, ldg, up, ldu, F, rows, y, ldy, stream);
+}
+
+int spiral_glu(int glu_op, int swapped, const float* x, int64_t ldx, int64_t F, int64_t rows, float* y, int64_t ldy,
+               void* stream) {
+  if (!glu_op_ok(glu_op)) return SPIRAL_ERR_TYPE;
+  return glu_entry(glu_op, swapped, 0.0f, 0.0f, x, ldx, F, rows, y, ldy, stream);
+}
+
+int spiral_glu_swiglu_oai(int swapped, float alpha, float limit, const float* x, int64_t ldx, int64_t F, int64_t rows,
+                          float* y, int64_t ldy, void* stream) {
+  return glu_entry(SPIRAL_GLU_SWIGLU_OAI, swapped, alpha, limit, x, ldx, F, rows, y, ldy, stream);
+}
+
+int spiral_glu_split_swiglu_oai(int swapped, float alpha, float limit, const float* gate, int64_t ldg,
+                                const float* up, int64_t ldu, int64_t F, int64_t rows, float* y, int64_t ldy,
+                                void* stream) {
+  return glu_split_entry(SPIRAL_GLU_SWIGLU_OAI, swapped, alpha, limit, gate, ldg, up, ldu, F, rows, y, ldy, stream);
 }
 
 }  // extern "C"

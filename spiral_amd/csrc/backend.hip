@@ -341,6 +341,20 @@ int compute_glu(spiral_backend* be, const spiral_tensor* t) {
   const spiral_tensor* a = t->src[0];
   const spiral_tensor* b2 = t->src[1];
   const int64_t rows = t->ne[1] * t->ne[2] * t->ne[3];
+  if (t->op_params[0] == SPIRAL_GLU_SWIGLU_OAI) {
+    // ggml keeps alpha and limit as floats in op_params[2] and [3].
+    float alpha, limit;
+    std::memcpy(&alpha, &t->op_params[2], sizeof alpha);
+    std::memcpy(&limit, &t->op_params[3], sizeof limit);
+    if (b2 != nullptr)
+      return spiral_glu_split_swiglu_oai(t->op_params[1], alpha, limit, static_cast<const float*>(a->data),
+                                         static_cast<int64_t>(a->nb[1] / 4), static_cast<const float*>(b2->data),
+                                         static_cast<int64_t>(b2->nb[1] / 4), t->ne[0], rows,
+                                         static_cast<float*>(t->data), static_cast<int64_t>(t->nb[1] / 4), be->stream);
+    return spiral_glu_swiglu_oai(t->op_params[1], alpha, limit, static_cast<const float*>(a->data),
+                                 static_cast<int64_t>(a->nb[1] / 4), t->ne[0], rows, static_cast<float*>(t->data),
+                                 static_cast<int64_t>(t->nb[1] / 4), be->stream);
+  }
   if (b2 != nullptr)
     return spiral_glu_split(t->op_params[0], t->op_params[1], static_cast<const float*>(a->data),
                             static_cast<int64_t>(a->nb[1] / 4), static_cast<const float*>(b2->data),
@@ -380,6 +394,7 @@ bool fusable_glu(const spiral_cgraph* graph, int32_t i) {
   const spiral_tensor* t = graph->nodes[i];
   const spiral_tensor* g = graph->nodes[i + 1];
   if (t->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU || g->src[0] != t || g->src[1] != nullptr) return false;
+  if (g->op_params[0] == SPIRAL_GLU_SWIGLU_OAI) return false;  // runs unfused (its own GLU entry point)
   if ((t->flags & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || !fully_contiguous(g, 4)) return false;
   const spiral_tensor* a = t->src[0];
   if (!spiral_mul_mat_id_glu_fits(a->type, a->ne[1], a->ne[0])) return false;
@@ -402,6 +417,7 @@ bool fusable_glu_split(const spiral_cgraph* graph, int32_t i) {
   const spiral_tensor* t1 = graph->nodes[i + 1];
   const spiral_tensor* g = graph->nodes[i + 2];
   if (t0->op != SPIRAL_OP_MUL_MAT_ID || t1->op != SPIRAL_OP_MUL_MAT_ID || g->op != SPIRAL_OP_GLU) return false;
+  if (g->op_params[0] == SPIRAL_GLU_SWIGLU_OAI) return false;  // runs unfused (its own GLU entry point)
   if (g->src[1] == nullptr || !((g->src[0] == t0 && g->src[1] == t1) || (g->src[0] == t1 && g->src[1] == t0)))
     return false;
   if (((t0->flags | t1->flags) & SPIRAL_TENSOR_FLAG_OUTPUT) != 0 || !fully_contiguous(g, 4)) return false;
@@ -653,7 +669,7 @@ int spiral_supports_op(const spiral_tensor* t) {
       if (a == nullptr) return 0;
       const int32_t op = t->op_params[0], swapped = t->op_params[1];
       if (op != SPIRAL_GLU_REGLU && op != SPIRAL_GLU_GEGLU && op != SPIRAL_GLU_SWIGLU && op != SPIRAL_GLU_GEGLU_ERF &&
-          op != SPIRAL_GLU_GEGLU_QUICK)
+          op != SPIRAL_GLU_GEGLU_QUICK && op != SPIRAL_GLU_SWIGLU_OAI)
         return 0;
       if (swapped != 0 && swapped != 1) return 0;
       for (const spiral_tensor* u : {a, b2, t}) {

@@ -849,17 +849,31 @@ __device__ __forceinline__ float glu_act(int op, float a) {
   }
 }
 
+// One output of a standalone GLU: act(a) * b, a the activated half. SWIGLU_OAI
+// (gpt-oss, as ggml computes it): with x = min(a, limit) and
+// y = clamp(b, -limit, limit), x / (1 + exp(-alpha x)) * (y + 1); min and
+// clamp written as comparisons, as std::min and std::clamp evaluate them.
+__device__ __forceinline__ float glu_pair(int op, float a, float b, float alpha, float limit) {
+  if (op == SPIRAL_GLU_SWIGLU_OAI) {
+    const float x = limit < a ? limit : a;
+    const float y = b < -limit ? -limit : (limit < b ? limit : b);
+    return x / (1.0f + expf(alpha * (-x))) * (y + 1.0f);
+  }
+  return glu_act(op, a) * b;
+}
+
 // Standalone ggml GLU over rows of 2n floats: y[r][i] = act(h0[i]) * h1[i]
 // with (h0, h1) = (x[r][0 .. n), x[r][n .. 2n)), swapped: the other order.
 __global__ void __launch_bounds__(256) glu_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ y,
-                                                  int64_t ldy, int64_t n, int64_t rows, int op, int swapped) {
+                                                  int64_t ldy, int64_t n, int64_t rows, int op, int swapped,
+                                                  float alpha, float limit) {
   const int64_t total = n * rows;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * 256) {
     const int64_t r = i / n, c = i - r * n;
     const float* xr = x + r * ldx;
     const float a = xr[swapped ? c + n : c], b = xr[swapped ? c : c + n];
-    y[r * ldy + c] = glu_act(op, a) * b;
+    y[r * ldy + c] = glu_pair(op, a, b, alpha, limit);
   }
 }
 
@@ -868,13 +882,13 @@ __global__ void __launch_bounds__(256) glu_kernel(const float* __restrict__ x, i
 __global__ void __launch_bounds__(256) glu_split_kernel(const float* __restrict__ xg, int64_t ldg,
                                                         const float* __restrict__ xu, int64_t ldu,
                                                         float* __restrict__ y, int64_t ldy, int64_t n, int64_t rows,
-                                                        int op, int swapped) {
+                                                        int op, int swapped, float alpha, float limit) {
   const int64_t total = n * rows;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * 256) {
     const int64_t r = i / n, c = i - r * n;
     const float g = xg[r * ldg + c], u = xu[r * ldu + c];
-    y[r * ldy + c] = swapped ? glu_act(op, u) * g : glu_act(op, g) * u;
+    y[r * ldy + c] = swapped ? glu_pair(op, u, g, alpha, limit) : glu_pair(op, g, u, alpha, limit);
   }
 }
 
@@ -1822,23 +1836,23 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
 // Standalone GLU over `rows` rows of 2n floats; arguments validated by the
 // caller.
 int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
-        hipStream_t s) {
+        hipStream_t s, float alpha, float limit) {
   const int64_t total = n * rows;
   if (total == 0) return SPIRAL_OK;
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 8 * static_cast<int64_t>(device_cu_count()));
   hipLaunchKernelGGL(glu_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, x, ldx, y, ldy, n, rows, op,
-                     swapped);
+                     swapped, alpha, limit);
   return launch_status();
 }
 
 // Split form: gate rows at xg (stride ldg), up rows at xu (stride ldu).
 int glu_split(int op, int swapped, const float* xg, int64_t ldg, const float* xu, int64_t ldu, int64_t n,
-              int64_t rows, float* y, int64_t ldy, hipStream_t s) {
+              int64_t rows, float* y, int64_t ldy, hipStream_t s, float alpha, float limit) {
   const int64_t total = n * rows;
   if (total == 0) return SPIRAL_OK;
   const int64_t blocks = std::min<int64_t>(ceil_div(total, 256), 8 * static_cast<int64_t>(device_cu_count()));
   hipLaunchKernelGGL(glu_split_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, xg, ldg, xu, ldu, y, ldy,
-                     n, rows, op, swapped);
+                     n, rows, op, swapped, alpha, limit);
   return launch_status();
 }
 

@@ -8,6 +8,7 @@ libspiral_quants.so on the device; nothing here computes.
 """
 
 import ctypes
+import struct
 
 from ._lib import (TYPE_BF16, TYPE_F16, TYPE_F32, TYPE_I32, TYPE_IQ4_NL, TYPE_IQ4_XS, TYPE_Q4_0,  # noqa: F401
                    TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_0, check, lib)
@@ -160,19 +161,27 @@ def mul_mat_id(a, b, ids, name="mul_mat_id"):
     return _node(TYPE_F32, [a.ne[1], ids.ne[0], ids.ne[1], 1], OP_MUL_MAT_ID, [a, b, ids], name)
 
 
-def glu(a, op=GLU_SWIGLU, swapped=False, name="glu"):
-    """ggml_glu(a, op, swapped) (single-tensor form): [a.ne0 / 2, a.ne1, ...] F32."""
-    t = _node(TYPE_F32, [a.ne[0] // 2, a.ne[1], a.ne[2], a.ne[3]], OP_GLU, [a], name)
+def _glu_params(t, op, swapped, alpha, limit):
     t.op_params[0] = op
     t.op_params[1] = int(swapped)
+    if op == GLU_SWIGLU_OAI:  # ggml_swiglu_oai: alpha and limit as float bits in op_params[2], [3]
+        t.op_params[2] = struct.unpack("<i", struct.pack("<f", alpha))[0]
+        t.op_params[3] = struct.unpack("<i", struct.pack("<f", limit))[0]
+
+
+def glu(a, op=GLU_SWIGLU, swapped=False, name="glu", alpha=1.702, limit=7.0):
+    """ggml_glu(a, op, swapped) (single-tensor form): [a.ne0 / 2, a.ne1, ...] F32;
+    SWIGLU_OAI as ggml_swiglu_oai with alpha and limit."""
+    t = _node(TYPE_F32, [a.ne[0] // 2, a.ne[1], a.ne[2], a.ne[3]], OP_GLU, [a], name)
+    _glu_params(t, op, swapped, alpha, limit)
     return t
 
 
-def glu_split(a, b, op=GLU_SWIGLU, swapped=False, name="glu_split"):
-    """ggml_glu_split(a, b, op) (split form): act(a) * b over equal shapes, F32."""
+def glu_split(a, b, op=GLU_SWIGLU, swapped=False, name="glu_split", alpha=1.702, limit=7.0):
+    """ggml_glu_split(a, b, op) (split form): act(a) * b over equal shapes, F32;
+    SWIGLU_OAI as ggml_swiglu_oai(a, b, alpha, limit)."""
     t = _node(TYPE_F32, list(a.ne), OP_GLU, [a, b], name)
-    t.op_params[0] = op
-    t.op_params[1] = int(swapped)
+    _glu_params(t, op, swapped, alpha, limit)
     return t
 
 

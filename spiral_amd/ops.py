@@ -119,7 +119,8 @@ def mul_mat_id(qtype, w, expert_stride, n_expert, n_rows, k, x, ids, out_dtype=t
     return out
 
 
-# ggml GLU variants (ggml_glu_op numbering); SWIGLU_OAI (3) is not implemented.
+# ggml GLU variants (ggml_glu_op numbering). SWIGLU_OAI (3) takes alpha and
+# limit (gpt-oss uses 1.702 and 7.0) and runs only as a standalone GLU.
 GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_GEGLU_ERF, GLU_GEGLU_QUICK = range(6)
 
 
@@ -165,9 +166,10 @@ def mul_mat_id_glu_split(qtype, w_gate, w_up, expert_stride, n_expert, n_ff, k, 
     return out
 
 
-def glu_split(gate, up, glu_op=GLU_SWIGLU, swapped=False, out=None):
+def glu_split(gate, up, glu_op=GLU_SWIGLU, swapped=False, out=None, alpha=1.702, limit=7.0):
     """ggml's split GLU over float32 tensors of equal shape [..., F]:
-    act(gate) * up (act(up) * gate when swapped)."""
+    act(gate) * up (act(up) * gate when swapped); alpha and limit are
+    SWIGLU_OAI's parameters."""
     _require_cuda(gate, up)
     if gate.dtype != torch.float32 or up.dtype != torch.float32 or gate.shape != up.shape:
         raise TypeError("glu_split takes two float32 tensors of one shape")
@@ -176,13 +178,18 @@ def glu_split(gate, up, glu_op=GLU_SWIGLU, swapped=False, out=None):
     F = g2.shape[1]
     if out is None:
         out = torch.empty(gate.shape, dtype=torch.float32, device=gate.device)
+    if glu_op == GLU_SWIGLU_OAI:
+        check(lib().spiral_glu_split_swiglu_oai(int(swapped), alpha, limit, _ptr(g2), F, _ptr(u2), F, F, g2.shape[0],
+                                                _ptr(out), F, _stream()), "glu_split_swiglu_oai")
+        return out
     check(lib().spiral_glu_split(glu_op, int(swapped), _ptr(g2), F, _ptr(u2), F, F, g2.shape[0], _ptr(out), F,
                                  _stream()), "glu_split")
     return out
 
 
-def glu(x, glu_op=GLU_SWIGLU, swapped=False, out=None):
-    """ggml GLU over the last dimension of a float32 tensor [..., 2F] -> [..., F]."""
+def glu(x, glu_op=GLU_SWIGLU, swapped=False, out=None, alpha=1.702, limit=7.0):
+    """ggml GLU over the last dimension of a float32 tensor [..., 2F] -> [..., F];
+    alpha and limit are SWIGLU_OAI's parameters."""
     _require_cuda(x)
     if x.dtype != torch.float32:
         raise TypeError("glu takes float32")
@@ -190,6 +197,10 @@ def glu(x, glu_op=GLU_SWIGLU, swapped=False, out=None):
     F = x2.shape[1] // 2
     if out is None:
         out = torch.empty(x.shape[:-1] + (F,), dtype=torch.float32, device=x.device)
+    if glu_op == GLU_SWIGLU_OAI:
+        check(lib().spiral_glu_swiglu_oai(int(swapped), alpha, limit, _ptr(x2), x2.shape[1], F, x2.shape[0],
+                                          _ptr(out), F, _stream()), "glu_swiglu_oai")
+        return out
     check(lib().spiral_glu(glu_op, int(swapped), _ptr(x2), x2.shape[1], F, x2.shape[0], _ptr(out), F, _stream()),
           "glu")
     return out

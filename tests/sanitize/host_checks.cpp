@@ -308,6 +308,13 @@ void check_validation() {
          "glu_split ld");
   EXPECT(spiral_glu_split(SPIRAL_GLU_SWIGLU, 0, nullptr, 8, ybuf, 8, 4, 2, ybuf, 8, nullptr) == SPIRAL_ERR_NULL,
          "glu_split null");
+  EXPECT(spiral_glu(SPIRAL_GLU_SWIGLU_OAI, 0, ybuf, 8, 4, 2, ybuf, 4, nullptr) == SPIRAL_ERR_TYPE, "glu oai plain");
+  EXPECT(spiral_glu_swiglu_oai(0, 1.702f, 7.0f, ybuf, big, big / 2 + 1, 2, ybuf, big, nullptr) != SPIRAL_OK,
+         "glu oai overflow");
+  EXPECT(spiral_glu_split_swiglu_oai(0, 1.702f, 7.0f, ybuf, big, ybuf, 8, 4, big, ybuf, 8, nullptr) != SPIRAL_OK,
+         "glu_split oai overflow");
+  EXPECT(spiral_glu_split_swiglu_oai(1, 1.702f, 7.0f, ybuf, 8, nullptr, 8, 4, 2, ybuf, 8, nullptr) ==
+             SPIRAL_ERR_NULL, "glu_split oai null");
   EXPECT(spiral_mul_mat_id_glu_split(q, wbuf, nullptr, 144, 4, 4, 32, xbuf, 1, ids, 4, 2, SPIRAL_GLU_SWIGLU, 0, ybuf,
                                      SPIRAL_TYPE_F32, wbuf, 4096, nullptr) == SPIRAL_ERR_NULL, "glu_split null up");
   EXPECT(spiral_mul_mat_id_glu_split(q, wbuf, wbuf, big, 4, big / 2 + 1, 32, xbuf, 1, ids, 4, 2, SPIRAL_GLU_SWIGLU, 0,

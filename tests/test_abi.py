@@ -154,10 +154,19 @@ def test_validation_before_device_work(spiral_lib):
     assert L.spiral_glu(7, 0, p, 8, 4, 2, p, 4, None) == 6
     assert L.spiral_glu(2, 0, p, 7, 4, 2, p, 4, None) == 1  # ldx < 2F
     assert L.spiral_glu(2, 0, p, 8, 4, 0, p, 4, None) == 0  # no rows: a no-op
+    # SWIGLU_OAI needs alpha and limit: its own entry points, TYPE from the plain ones
+    assert L.spiral_glu(3, 0, p, 8, 4, 2, p, 4, None) == 6
+    assert L.spiral_glu_split(3, 0, p, 4, p, 4, 4, 2, p, 4, None) == 6
+    assert L.spiral_glu_swiglu_oai(2, 1.702, 7.0, p, 8, 4, 2, p, 4, None) == 6  # swapped not 0 / 1
+    assert L.spiral_glu_swiglu_oai(0, 1.702, 7.0, p, 7, 4, 2, p, 4, None) == 1  # ldx < 2F
+    assert L.spiral_glu_swiglu_oai(0, 1.702, 7.0, p, 8, 4, 0, p, 4, None) == 0  # no rows
+    assert L.spiral_glu_split_swiglu_oai(0, 1.702, 7.0, p, 3, p, 4, 4, 2, p, 4, None) == 1  # ldg < F
+    assert L.spiral_glu_split_swiglu_oai(0, 1.702, 7.0, None, 4, p, 4, 4, 2, p, 4, None) == 3
     if L.spiral_device_count() == 0:
         assert L.spiral_mul_mat_id_glu(q4, p, 144, 4, 4, 64, p, 1, p, 2, 2, 2, 0, p, _lib.TYPE_F32, p, 1 << 20,
                                        None) == 4
         assert L.spiral_glu(2, 1, p, 8, 4, 2, p, 4, None) == 4
+        assert L.spiral_glu_swiglu_oai(1, 1.702, 7.0, p, 8, 4, 2, p, 4, None) == 4
         assert L.spiral_dequant_bf16(q4, p, 4, 64, p, 64, None) == 4
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 1, p, _lib.TYPE_F32, 4, None, 0, None) == 4
         assert L.spiral_mul_mat(q4, p, 4, 64, p, 64, 20, p, _lib.TYPE_F32, 4, p, 8192, None) == 4

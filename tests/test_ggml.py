@@ -10,6 +10,7 @@ GLU over it) against the oracle.
 """
 
 import ctypes
+import struct
 
 import numpy as np
 import pytest
@@ -84,7 +85,13 @@ def test_supports_op_glu(spiral_lib):
             g = ggml.glu(h, op, swapped)
             assert list(g.ne) == [96, 3, 5, 1]
             assert ggml.supports_op(g)
-    assert not ggml.supports_op(ggml.glu(h, ggml.GLU_SWIGLU_OAI))  # float parameters: not implemented
+    # SWIGLU_OAI: alpha and limit ride in op_params[2] and [3] as float bits
+    oai = ggml.glu(h, ggml.GLU_SWIGLU_OAI, alpha=1.702, limit=7.0)
+    assert ggml.supports_op(oai)
+    assert struct.unpack("<ff", struct.pack("<ii", oai.op_params[2], oai.op_params[3])) == (
+        struct.unpack("<f", struct.pack("<f", 1.702))[0], 7.0)
+    hs = ggml.new_tensor(ggml.TYPE_F32, [96, 3, 5])
+    assert ggml.supports_op(ggml.glu_split(hs, hs, ggml.GLU_SWIGLU_OAI, True))
     g = ggml.glu(h)
     g.op_params[1] = 2
     assert not ggml.supports_op(g)
@@ -365,6 +372,63 @@ def test_mul_mat_id_then_glu_fused_and_not(cuda):
     rows = np.frombuffer(bytes(out), dtype=np.float32).reshape(n_tokens, top_k, F + pad)
     assert rows[:, :, :F].tobytes() == y.tobytes()
     assert (rows[:, :, F:] == 5.0).all()
+    be.free()
+    buf.free()
+
+
+@pytest.mark.gpu
+def test_mul_mat_id_then_swiglu_oai(cuda):
+    """ggml_swiglu_oai over MUL_MAT_ID output, in the single-tensor form and
+    the split form (separate gate and up expert stacks): graph_compute runs
+    the products and the GLU as separate nodes (no fused form takes alpha and
+    limit), and the result matches the float64 oracle of each product
+    followed by SWIGLU_OAI. Outputs are scaled so both halves cross
+    +-limit."""
+    qtype, k, F, n_expert, top_k, n_tokens = O.Q4_0, 128, 32, 4, 2, 6
+    alpha, limit = 1.702, 3.0
+    raws = [synth.make_weights(qtype, 2 * F, k, 90 + e) for e in range(n_expert)]
+    rng = np.random.default_rng(19)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    xf = (40.0 * rng.standard_normal((n_tokens, 1, k))).astype(np.float32)
+    xb = synth.bf16_bits(xf[:, 0])
+    buf = ggml.Buffer(4 << 20)
+    a = buf.alloc(ggml.new_tensor(qtype, [k, 2 * F, n_expert]))
+    buf.set(a, np.concatenate(raws).tobytes())
+    b = buf.alloc(ggml.new_tensor(ggml.TYPE_F32, [k, 1, n_tokens]))
+    buf.set(b, xf.tobytes())
+    it = buf.alloc(ggml.new_tensor(ggml.TYPE_I32, [top_k, n_tokens]))
+    buf.set(it, ids.tobytes())
+    prod = buf.alloc(ggml.mul_mat_id(a, b, it))
+    g = buf.alloc(ggml.glu(prod, ggml.GLU_SWIGLU_OAI, alpha=alpha, limit=limit))
+    assert ggml.supports_op(g)
+    sentinel = np.full(2 * F * top_k * n_tokens, 7.0, dtype=np.float32).tobytes()
+    buf.set(prod, sentinel)
+    be = ggml.Backend(0)
+    assert be.graph_compute([prod, g]) == 0
+    be.synchronize()
+    assert buf.get(prod) != sentinel  # not fused: the product was written
+    y = np.frombuffer(buf.get(g), dtype=np.float32).reshape(n_tokens, top_k, F)
+    p = np.frombuffer(buf.get(prod), dtype=np.float32).reshape(n_tokens, top_k, 2 * F)
+    assert np.abs(p).max() > limit and (p[..., :F] > limit).any() and (p[..., F:] < -limit).any()
+    for t in range(n_tokens):
+        for s in range(top_k):
+            p_ref = O.matmul_f64(O.dequant(qtype, raws[ids[t, s]], 2 * F, k), xb[t][None])[0]
+            want = O.glu_f64(p_ref, O.GLU_SWIGLU_OAI, alpha=alpha, limit=limit)
+            assert rel_err(y[t, s], want) <= REL_TOL
+    # The split form: gate and up experts in two tensors, two MUL_MAT_ID nodes.
+    ag = buf.alloc(ggml.new_tensor(qtype, [k, F, n_expert]))
+    au = buf.alloc(ggml.new_tensor(qtype, [k, F, n_expert]))
+    rb = O.row_bytes(qtype, k)
+    buf.set(ag, b"".join(r[: F * rb].tobytes() for r in raws))
+    buf.set(au, b"".join(r[F * rb:].tobytes() for r in raws))
+    pg = buf.alloc(ggml.mul_mat_id(ag, b, it))
+    pu = buf.alloc(ggml.mul_mat_id(au, b, it))
+    gs = buf.alloc(ggml.glu_split(pg, pu, ggml.GLU_SWIGLU_OAI, alpha=alpha, limit=limit))
+    assert ggml.supports_op(gs)
+    assert be.graph_compute([pg, pu, gs]) == 0
+    be.synchronize()
+    ys = np.frombuffer(buf.get(gs), dtype=np.float32).reshape(n_tokens, top_k, F)
+    assert ys.tobytes() == y.tobytes()  # same products, same GLU: the same bits
     be.free()
     buf.free()
 

@@ -46,6 +46,26 @@ def test_glu_split_standalone(cuda):
             assert rel_err(y, want) <= 1e-5, (op, swapped)
 
 
+def test_glu_swiglu_oai_standalone(cuda):
+    """SWIGLU_OAI (gpt-oss's GLU) over merged [.., 2F] rows and over separate
+    gate / up tensors, both half orders, inputs well past +-limit (the
+    activated half capped from above, the other clamped both ways), at
+    gpt-oss's alpha 1.702 / limit 7 and at alpha 1 / limit 3, against the
+    oracle's float64 form; both forms give the same bits."""
+    rng = np.random.default_rng(33)
+    g = (6.0 * rng.standard_normal((4, 3, 56))).astype(np.float32)
+    u = (6.0 * rng.standard_normal((4, 3, 56))).astype(np.float32)
+    gt, ut = torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda)
+    merged = torch.from_numpy(np.concatenate([g, u], axis=-1)).to(cuda)
+    for alpha, limit in ((1.702, 7.0), (1.0, 3.0)):
+        for swapped in (False, True):
+            want = O.glu_f64(np.concatenate([g, u], axis=-1), O.GLU_SWIGLU_OAI, swapped, alpha=alpha, limit=limit)
+            y1 = ops.glu_split(gt, ut, ops.GLU_SWIGLU_OAI, swapped, alpha=alpha, limit=limit).cpu().numpy()
+            y2 = ops.glu(merged, ops.GLU_SWIGLU_OAI, swapped, alpha=alpha, limit=limit).cpu().numpy()
+            assert rel_err(y1, want) <= 1e-5, (alpha, limit, swapped, rel_err(y1, want))
+            assert np.array_equal(y1, y2)
+
+
 @pytest.mark.parametrize("qtype", FORMATS)
 def test_fused_split_matches_unfused_and_oracle(cuda, qtype):
     """Every format: the fused split pass equals MUL_MAT_ID of each stack and

@@ -370,6 +370,30 @@ def test_glu_oracle_closed_forms():
         assert np.array_equal(O.glu_f64(h, op, swapped=True), O.glu_f64(np.concatenate([b, a]), op))
 
 
+def test_glu_swiglu_oai_closed_forms():
+    """SWIGLU_OAI against what fixes it: with no limit it is SWIGLU (alpha 1)
+    and GEGLU_QUICK (alpha 1.702) of a times b + 1; a is capped at limit (not
+    below), b clamped to [-limit, limit]; zero at a = 0 and at b = -1; swapped
+    exchanges the halves. A dropped + 1, a clamp on the wrong side or a lost
+    alpha fails one of these."""
+    a = np.array([-6.0, -1.5, 0.0, 0.7, 2.0, 9.0])
+    b = np.array([3.0, -0.25, 4.0, 1.0, -1.0, 0.5])
+    h = np.concatenate([a, b])
+    hb = np.concatenate([a, b + 1.0])
+    oai = lambda hh, alpha, limit, **kw: O.glu_f64(hh, O.GLU_SWIGLU_OAI, alpha=alpha, limit=limit, **kw)
+    assert np.allclose(oai(h, 1.0, np.inf), O.glu_f64(hb, O.GLU_SWIGLU), rtol=1e-15)
+    assert np.allclose(oai(h, 1.702, np.inf), O.glu_f64(hb, O.GLU_GEGLU_QUICK), rtol=1e-15)
+    got = oai(h, 1.702, 7.0)
+    sig = lambda z: 1.0 / (1.0 + math.exp(-z))
+    assert math.isclose(got[5], 7.0 * sig(1.702 * 7.0) * 1.5, rel_tol=1e-15)  # a = 9 capped at 7
+    assert math.isclose(got[0], -6.0 * sig(-1.702 * 6.0) * 4.0, rel_tol=1e-15)  # a = -6 kept (no lower cap)
+    assert got[2] == 0.0 and got[4] == 0.0
+    clamp = oai(np.array([1.0, 1.0, 50.0, -50.0]), 1.702, 7.0)
+    assert math.isclose(clamp[0], sig(1.702) * 8.0, rel_tol=1e-15)   # b = 50 -> 7, times (7 + 1)
+    assert math.isclose(clamp[1], sig(1.702) * -6.0, rel_tol=1e-15)  # b = -50 -> -7, times (-7 + 1)
+    assert np.array_equal(oai(h, 1.702, 7.0, swapped=True), oai(np.concatenate([b, a]), 1.702, 7.0))
+
+
 # ---- the CPU baseline bench.py times (oracle/cpu_baseline.c) ---------------------
 
 def test_cpu_baseline_matches_the_oracle(oracle):
