@@ -18,12 +18,18 @@ Measurement
     copies of its weights to exceed the 256 MB Infinity Cache twice over, so
     successive launches read HBM, not the last-level cache.
   - A "step" is one launch of the workload's kernel(s). W warm-up steps, then
-    K steps captured in a HIP graph and replayed three times untimed and once timed.
-    A HIP event pair on the replay stream brackets the timed replay:
-    "ms_per_step" is its duration / K, "value" is K steps of algorithmic work
-    over it (whole-job throughput, inputs resident in HBM), and
-    "roofline.achieved" is the algorithmic bytes (or FLOPs) of one launch over
-    the mean step. "wall_ms_per_step" is the host clock around the same replay.
+    K steps launched back to back and timed by one HIP event pair on the
+    launch stream, between two device synchronizations. The host issues the
+    K launches while an untimed pre-roll kernel (a bounded device spin, sized
+    from the host's measured issue time) keeps the GPU busy, so the timed
+    window holds the K steps and not the host's launch latency; a run whose
+    start event completed before the last launch was issued is repeated with
+    a longer pre-roll. "ms_per_step" is the window / K, "value" is K steps of
+    algorithmic work over it (whole-job throughput, inputs resident in HBM),
+    and "roofline.achieved" is the algorithmic bytes (or FLOPs) of one launch
+    over the mean step. One untimed pre-rolled run of K steps precedes the
+    timed one. "issue_us_per_step" is the host's time to issue one step
+    (measured over K untimed launches), which the pre-roll hides.
   - "roofline.traffic" is the HBM bytes one launch of the workload's kernel
     moves, from rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE runs of this
     script, each scaled by the factor that makes a plain 256 MiB device copy
@@ -39,7 +45,7 @@ Measurement
     repeated for --cpu-seconds split across the legs; each records nproc,
     the usable CPUs, OMP_NUM_THREADS and the CPU model.
   - "step_us_replays": p10 / p50 / p90 of the step time over ten further
-    timed replays of the same K-launch graph (not part of "value").
+    timed runs of K steps, each behind its own pre-roll (not part of "value").
 """
 
 import argparse
@@ -79,53 +85,76 @@ def copies_for(bytes_per_step):
 
 
 class Timer:
-    """W eager warm-up launches, then K launches captured in one HIP graph.
+    """W eager warm-up launches, then K launches timed back to back.
 
-    The graph is replayed three times untimed (upload and settling), then once timed: a HIP event
-    pair on the replay stream brackets the K launches, between two device
-    synchronizations. Returns (wall seconds, event seconds) of the timed
-    replay; event seconds / K is the mean duration of one step."""
+    Before each timed run the device is synchronized and an untimed pre-roll
+    (torch.cuda._sleep, a bounded spin) is queued; the start event, the K
+    launches and the end event follow while it runs, so the event window
+    holds the K steps and none of the host's issue time. The pre-roll lasts
+    twice the host's measured issue time for K launches plus 0.2 ms; if the
+    start event has already completed when the last launch is issued, the
+    run is repeated with a pre-roll twice as long. One untimed run of the
+    same kind comes first (clocks settle after the spin), then the timed
+    one. Returns (host issue seconds for K launches, event seconds) of the
+    timed run; "spread" holds the per-step time of ten further runs."""
 
     def __init__(self, torch, replays=10):
         self.torch = torch
         self.replays = replays
         self.spread = []
+        self._cps = None
+
+    def _cycles_per_s(self):
+        """Rate of the pre-roll's spin counter (measured once)."""
+        if self._cps is None:
+            torch = self.torch
+            torch.cuda._sleep(1000)
+            torch.cuda.synchronize()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            torch.cuda._sleep(2_000_000)
+            b.record()
+            torch.cuda.synchronize()
+            self._cps = 2_000_000 / max(a.elapsed_time(b) * 1e-3, 1e-6)
+        return self._cps
+
+    def _timed(self, launch, steps, preroll_s):
+        torch = self.torch
+        stream = torch.cuda.current_stream()
+        for _ in range(4):
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(preroll_s * self._cycles_per_s()))
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            t0 = time.perf_counter()
+            for i in range(steps):
+                launch(i)
+            end.record(stream)
+            late = start.query()  # the GPU reached the window before the last launch was issued
+            issue = time.perf_counter() - t0
+            torch.cuda.synchronize()
+            if not late:
+                break
+            preroll_s *= 2
+        return issue, start.elapsed_time(end) * 1e-3
 
     def run(self, launch, steps, warmup):
         torch = self.torch
         for i in range(warmup):
             launch(i)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(steps):
-                launch(i)
-        for _ in range(3):  # upload, then two more untimed replays (clocks and caches settle)
-            g.replay()
+        t0 = time.perf_counter()  # the host's issue time for K launches, untimed on the device
+        for i in range(steps):
+            launch(i)
+        issue = time.perf_counter() - t0
         torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        start.record(stream)
-        g.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ev = start.elapsed_time(end) * 1e-3
-        # Further timed replays of the same graph, for the spread of the step
-        # time (each a mean over K launches; not part of "value").
-        self.spread = []
-        for _ in range(self.replays):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            g.replay()
-            b.record(stream)
-            torch.cuda.synchronize()
-            self.spread.append(a.elapsed_time(b) * 1e-3 / steps)
-        del g
-        return wall, ev
+        preroll = min(0.05, 2.0 * issue + 2e-4)
+        self._timed(launch, steps, preroll)  # untimed: the same sequence once, clocks settling
+        _, ev = self._timed(launch, steps, preroll)
+        self.spread = [self._timed(launch, steps, preroll)[1] / steps for _ in range(self.replays)]
+        return issue, ev
 
 
 def traffic_table():
@@ -301,12 +330,12 @@ def main():
         x = synth.make_x(m, k, seed)
         return x, torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(dev)
 
-    def record(name, wall, ev, per_launch, unit, peak, bound, extra=None):
+    def record(name, issue, ev, per_launch, unit, peak, bound, extra=None):
         scale = 1e9 if unit == "GB/s" else 1e12
         step = ev / steps
         achieved = per_launch / step / scale
         r = {"value": per_launch * steps / ev / scale, "unit": unit, "ms_per_step": step * 1e3,
-             "wall_ms_per_step": wall / steps * 1e3, "step_us": step * 1e6,
+             "issue_us_per_step": issue / steps * 1e6, "step_us": step * 1e6,
              "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                           "frac": achieved / peak}}
         if timer.spread:
@@ -327,8 +356,8 @@ def main():
         raw, ws = upload_planar(TYPE_Q8_0, n, k, 1, copies_for(wbytes))
         x, xd = x_dev(1, k, 2)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q8_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("gemv_q8_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        issue, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q8_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q8_0", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q8_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         cpu_inputs["gemv_q8_0"] = (raw, x)
@@ -341,8 +370,8 @@ def main():
         _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies_for(wbytes))
         _, xd = x_dev(1, k, 4)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q6_K, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("gemv_q6_k", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        issue, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q6_K, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q6_k", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q6_K decode GEMV y[4096] = W[4096x14336] x[14336], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
@@ -354,8 +383,8 @@ def main():
         _, ws = upload_planar(TYPE_Q4_0, n, k, 5, copies_for(wbytes))
         _, xd = x_dev(1, k, 6)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("gemv_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        issue, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("gemv_q4_0", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
@@ -370,8 +399,8 @@ def main():
         _, ws = upload_planar(qt, n, k, 21, copies_for(wbytes))
         _, xd = x_dev(1, k, 22)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
-        wall, ev = timer.run(lambda i: ops.mul_mat(qt, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record(wl, wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        issue, ev = timer.run(lambda i: ops.mul_mat(qt, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record(wl, issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": f"{qname.upper()} decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
@@ -384,8 +413,8 @@ def main():
         _, ws = upload_planar(TYPE_Q4_0, n, k, 11, copies_for(wbytes))
         _, xd = x_dev(m, k, 12)
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
-        record("mul_mat_q4_0_m4", wall, ev, step_bytes, "GB/s", HBM_PEAK_GBS, "hbm",
+        issue, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
+        record("mul_mat_q4_0_m4", issue, ev, step_bytes, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 small-batch product Y[4x14336] = X[4x4096] W[14336x4096]^T, bf16 MFMA, "
                             "fp32 acc, bf16 out",
                 "bytes_per_launch": step_bytes, "copies": len(ws)})
@@ -400,9 +429,9 @@ def main():
         raw0, ws = upload_planar(TYPE_Q4_0, n, k, 0, copies)
         cpu_inputs["dequant_q4_0"] = (raw0,)
         outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
-        wall, ev = timer.run(lambda i: ops.dequant(TYPE_Q4_0, ws[i % copies], n, k, out=outs[i % copies]),
+        issue, ev = timer.run(lambda i: ops.dequant(TYPE_Q4_0, ws[i % copies], n, k, out=outs[i % copies]),
                                steps, warmup)
-        record("dequant_q4_0", wall, ev, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
+        record("dequant_q4_0", issue, ev, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q4_0 -> bf16 dequant, 4096x4096 (524,288 blocks)",
                 "bytes_per_launch": inb + outb, "packed_bytes": inb, "copies": copies})
         results["dequant_q4_0"]["packed_GBps"] = inb / (ev / steps) / 1e9
@@ -416,9 +445,9 @@ def main():
         copies = copies_for(inb + outb)
         _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies)
         outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
-        wall, ev = timer.run(lambda i: ops.dequant(TYPE_Q6_K, ws[i % copies], n, k, out=outs[i % copies]),
+        issue, ev = timer.run(lambda i: ops.dequant(TYPE_Q6_K, ws[i % copies], n, k, out=outs[i % copies]),
                                steps, warmup)
-        record("dequant_q6_k", wall, ev, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
+        record("dequant_q6_k", issue, ev, inb + outb, "GB/s", HBM_PEAK_GBS, "hbm",
                {"workload": "Q6_K -> bf16 dequant, 4096x14336 (229,376 super-blocks)",
                 "bytes_per_launch": inb + outb, "packed_bytes": inb, "copies": copies})
         results["dequant_q6_k"]["packed_GBps"] = inb / (ev / steps) / 1e9
@@ -436,9 +465,9 @@ def main():
         y = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         gws = ops.mul_mat_workspace(TYPE_Q4_0, n, k, m, dev)
         flops = 2.0 * m * n * k
-        wall, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y,
+        issue, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q4_0, ws[i % copies], n, k, xs[i % copies], out=y,
                                                    workspace=gws), steps, warmup)
-        record("gemm_q4_0", wall, ev, flops, "TFLOP/s", MFMA_BF16_PEAK_TFS, "mfma",
+        record("gemm_q4_0", issue, ev, flops, "TFLOP/s", MFMA_BF16_PEAK_TFS, "mfma",
                {"workload": "Q4_0 prefill dequant-GEMM Y[512x4096] = X[512x4096] W[4096x4096]^T, bf16 MFMA, fp32 acc "
                             "(one step = X packing + GEMM kernel)",
                 "flops_per_launch": flops, "copies": copies})
@@ -482,10 +511,10 @@ def main():
             ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, x2, ids_d, workspace=ws2, out=y2)
 
         if want("moe_q4_0"):
-            wall, ev = timer.run(launch, steps, warmup)
+            issue, ev = timer.run(launch, steps, warmup)
             wbytes = touched * (gu_per + dn_per)
             flops = 2.0 * n_tokens * top_k * (inter2 * hidden + hidden * inter)
-            record("moe_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+            record("moe_q4_0", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                    {"workload": "Q4_0 MoE: 128 experts (gate_up 1536x2048, down 2048x768), 64 tokens, top-8; "
                                 "one step = gate_up + down MUL_MAT_ID",
                     "bytes_per_launch": wbytes, "touched_experts": int(touched),
@@ -499,9 +528,9 @@ def main():
                 ops.mul_mat_id_glu(TYPE_Q4_0, gus[i % copies], gu_per, n_expert, inter2, hidden, x1, ids_d,
                                    ops.GLU_SWIGLU, workspace=ws1, out=h)
 
-            wall, ev = timer.run(launch_glu, steps, warmup)
+            issue, ev = timer.run(launch_glu, steps, warmup)
             wbytes = touched * gu_per
-            record("moe_gate_up_swiglu_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+            record("moe_gate_up_swiglu_q4_0", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                    {"workload": "Q4_0 MoE gate_up (128 experts of 1536x2048, 64 tokens, top-8) fused with SwiGLU "
                                 "into the [64][8][768] bf16 down-stage input; one step = one fused MUL_MAT_ID + GLU",
                     "bytes_per_launch": wbytes, "touched_experts": int(touched), "copies": copies})
@@ -528,11 +557,11 @@ def main():
                 ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, px2, pids_d, workspace=pws2,
                                out=py2)
 
-            wall, ev = timer.run(launch_prefill, steps, warmup)
+            issue, ev = timer.run(launch_prefill, steps, warmup)
             ptouched = np.unique(pids).size
             wbytes = ptouched * (gu_per + dn_per)
             flops = 2.0 * pt * top_k * (inter2 * hidden + hidden * inter)
-            record("moe_prefill_q4_0", wall, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+            record("moe_prefill_q4_0", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
                    {"workload": "Q4_0 MoE prefill: 128 experts (gate_up 1536x2048, down 2048x768), 1024 tokens, "
                                 "top-8 (64 pairs an expert on average); one step = gate_up + down MUL_MAT_ID",
                     "bytes_per_launch": wbytes, "touched_experts": int(ptouched),
