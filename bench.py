@@ -93,7 +93,8 @@ class Timer:
     holds the K steps and none of the host's issue time. The pre-roll lasts
     twice the host's measured issue time for K launches plus 0.2 ms; if the
     start event has already completed when the last launch is issued, the
-    run is repeated with a pre-roll twice as long. One untimed run of the
+    run is repeated with a pre-roll twice as long, and the workload's later
+    runs keep that length. One untimed run of the
     same kind comes first (clocks settle after the spin), then the timed
     one. Returns (host issue seconds for K launches, event seconds) of the
     timed run; "spread" holds the per-step time of ten further runs."""
@@ -102,6 +103,7 @@ class Timer:
         self.torch = torch
         self.replays = replays
         self.spread = []
+        self.preroll = 0.0
         self._cps = None
 
     def _cycles_per_s(self):
@@ -138,6 +140,7 @@ class Timer:
             if not late:
                 break
             preroll_s *= 2
+        self.preroll = preroll_s  # later runs start from the length that sufficed
         return issue, start.elapsed_time(end) * 1e-3
 
     def run(self, launch, steps, warmup):
@@ -150,10 +153,10 @@ class Timer:
             launch(i)
         issue = time.perf_counter() - t0
         torch.cuda.synchronize()
-        preroll = min(0.05, 2.0 * issue + 2e-4)
-        self._timed(launch, steps, preroll)  # untimed: the same sequence once, clocks settling
-        _, ev = self._timed(launch, steps, preroll)
-        self.spread = [self._timed(launch, steps, preroll)[1] / steps for _ in range(self.replays)]
+        self.preroll = min(0.05, 2.0 * issue + 2e-4)
+        self._timed(launch, steps, self.preroll)  # untimed: the same sequence once, clocks settling
+        _, ev = self._timed(launch, steps, self.preroll)
+        self.spread = [self._timed(launch, steps, self.preroll)[1] / steps for _ in range(self.replays)]
         return issue, ev
 
 
