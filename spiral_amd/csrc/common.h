@@ -97,9 +97,27 @@ struct PlanarKQ {
 // +0, exponent 31 gives the finite 2^16 * (1.m), otherwise IEEE binary16.
 // Written as an integer select so it compiles to v_cndmask, not a branch.
 __device__ __forceinline__ float fp16_scale(uint32_t h) {
-  const uint32_t e = h & 0x7c00u;
-  const uint32_t bits = ((h & 0x8000u) << 16) | (((h & 0x7fffu) << 13) + 0x38000000u);
-  return __uint_as_float(e ? bits : 0u);
+  const uint32_t t = h & 0x7fffu;
+  const uint32_t bits = ((h << 16) & 0x80000000u) | ((t << 13) + 0x38000000u);
+  return __uint_as_float(t >= 0x400u ? bits : 0u);
+}
+
+// The same decode for a scale that only ever multiplies codes inside an FMA
+// with its offset term (code * s - c * s, both exact): the hardware
+// conversion agrees with fp16_scale on exponents 1..30, and its -0 for a
+// -0 scale still gives every code a +0 weight. Exponents 0 (non-zero
+// mantissa: the hardware keeps the subnormal) and 31 (inf / NaN there) are
+// the reference's special cases; a wave in which any lane holds one takes
+// the bit-level decode for all its lanes (a wave-uniform branch), so the
+// common path costs one conversion and one class test instead of six
+// instructions.
+__device__ __forceinline__ float fp16_scale_fma(uint32_t h) {
+  const _Float16 hf = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h));
+  // v_cmp_class mask: signaling and quiet NaN, -inf, -subnormal, +subnormal, +inf
+  constexpr int kSpecial = 0x001 | 0x002 | 0x004 | 0x010 | 0x080 | 0x200;
+  float f = static_cast<float>(hf);
+  if (__builtin_amdgcn_ballot_w64(__builtin_amdgcn_classh(hf, kSpecial)) != 0) f = fp16_scale(h);
+  return f;
 }
 
 // IEEE binary16 -> float (subnormals keep their value): the K-quants' d and

@@ -200,15 +200,20 @@ struct MoePiece;
 
 // Q4_0: piece = block 4 kb + g. MFMA s takes qs dword s: its low nibbles
 // (elements 4s .. 4s + 3) then its high nibbles (16 + 4s .. 16 + 4s + 3).
+// A high nibble c is taken in place (byte 16 c, fp16 1024 + 16 c) against
+// the scale m / 16 and offset -72 m: (1024 + 16 c) m / 16 - 72 m = (c - 8) m,
+// exact inside the FMA as for the low nibbles, with no shift.
 template <>
 struct MoePiece<SPIRAL_TYPE_Q4_0> {
   uint4 q;
   uint32_t d;
-  float m, off;  // decoded scale and offset (prep)
+  float m, off, m16, off16;  // decoded scale and offsets (prep)
   static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
   __device__ __forceinline__ void prep() {
-    m = fp16_scale(d);
+    m = fp16_scale_fma(d);
     off = -1032.0f * m;
+    m16 = 0.0625f * m;
+    off16 = -72.0f * m;
   }
   // blk = block index of the lane's piece within the row's planar planes
   __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t blk) {
@@ -218,18 +223,23 @@ struct MoePiece<SPIRAL_TYPE_Q4_0> {
   __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
   __device__ __forceinline__ uint4 dequant(int s) const {
     const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
-    const float df = m;
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    uint32_t o[4];
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
+    // all eight products first, then the packs: a pack right behind the FMA
+    // that feeds it costs a wait state
+    float v[8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const uint32_t c = i ? hi : lo;
+      const float df = i ? m16 : m, of = i ? off16 : off;
       const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
       const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), df, off), __builtin_fmaf(static_cast<float>(a.y), df, off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), df, off), __builtin_fmaf(static_cast<float>(b.y), df, off));
+      v[4 * i] = __builtin_fmaf(static_cast<float>(a.x), df, of);
+      v[4 * i + 1] = __builtin_fmaf(static_cast<float>(a.y), df, of);
+      v[4 * i + 2] = __builtin_fmaf(static_cast<float>(b.x), df, of);
+      v[4 * i + 3] = __builtin_fmaf(static_cast<float>(b.y), df, of);
     }
-    return make_uint4(o[0], o[1], o[2], o[3]);
+    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                      pack_bf16x2(v[6], v[7]));
   }
 };
 
@@ -911,6 +921,13 @@ template <int TYPE, bool GLU, int TB>
 constexpr int kStreamWaves = (TB >= 2 && !GLU && !(TYPE == SPIRAL_TYPE_Q6_K && TB == 4)) ? 12 : 8;
 constexpr int64_t kStreamMaxK = 4096;
 
+// Waves per SIMD the compiler must leave room for (launch bounds). Decode
+// passes (TB = 1, 8-wave workgroups) are held to four, so two workgroups
+// share a CU (their staged rows fit its LDS twice): the Q4_0 fused GLU form
+// would otherwise take 130 registers and fit one. Q6_K would spill there.
+template <int TYPE, int TB, int WAVES>
+constexpr int kStreamMinWaves = (TB == 1 && WAVES == 8 && TYPE != SPIRAL_TYPE_Q6_K) ? 4 : 1;
+
 // Ring slots (units) in flight per wave.
 template <int TYPE>
 constexpr int kStreamRing = TYPE == SPIRAL_TYPE_Q4_0 ? 4 : TYPE == SPIRAL_TYPE_Q8_0 ? 6 : 4;
@@ -1059,46 +1076,39 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
   static constexpr int kSteps = 2;
   // As loaded, lane l = 32 h + 4 r' + c': qa / qb hold rows r' and 8 + r'
   // of the group, block 8 u + 4 h + c' (arrange() regroups them by step).
-  // Lane l = 32 h + 2 r + p: dl / dh hold the dwords around d of blocks
-  // 8 u + 4 h + 2 p and + 1 of row r.
+  // d0 / d1 are already in MFMA lane order: lane (r, g) = (l % 16, l / 16)
+  // holds the dword that contains the fp16 d of block 8 u + g (d0) and
+  // 8 u + 4 + g (d1) of row r, in its half dsh / 16.
   uint4 qa, qb;
-  uint32_t dl, dh;
-  int32_t dinfo;  // 4 (first of the two blocks - nb) + byte offset of its d in dl
+  uint32_t d0, d1;
+  uint32_t dsh;  // 0 or 16
   struct Addr {
-    uint32_t qa, qb, d;
-    int dc;
+    uint32_t qa, qb, d, dsh;
   };
   static __device__ __forceinline__ Addr addr(int64_t row0, int64_t n_rows, int64_t nb, int lane) {
     Addr a;
-    const int h = lane >> 5, c = 4 * h + (lane & 3), rq = (lane & 31) >> 2, rd = (lane & 31) >> 1;
-    a.dc = 4 * h + 2 * (lane & 1);
+    const int h = lane >> 5, c = 4 * h + (lane & 3), rq = (lane & 31) >> 2;
     a.qa = static_cast<uint32_t>((min(row0 + rq, n_rows - 1) * nb + c) * 16);
     a.qb = static_cast<uint32_t>((min(row0 + 8 + rq, n_rows - 1) * nb + c) * 16);
-    a.d = static_cast<uint32_t>((min(row0 + rd, n_rows - 1) * nb + a.dc) * 2);
+    const uint32_t od = static_cast<uint32_t>((min(row0 + (lane & 15), n_rows - 1) * nb + (lane >> 4)) * 2);
+    a.d = od & ~3u;
+    a.dsh = (od & 2u) << 3;
     return a;
   }
   // Every load is issued and every value is a whole loaded dword (a load
   // under a branch, or a narrower load whose widening the compiler places
-  // elsewhere, makes it wait for all of the ring's loads at once). The pair
-  // of fp16 d sits at an even byte offset: the two dwords around it are
-  // loaded and joined in piece(). Blocks past nb get d = 0 there, so their
-  // pieces are zero whatever their codes (the next row's bytes, or zero past
-  // the plane).
-  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t nb) {
-    const int64_t b = 8 * u;
-    const uint32_t sq = static_cast<uint32_t>(b * 16), sd = static_cast<uint32_t>(b * 2);
+  // elsewhere, makes it wait for all of the ring's loads at once). Blocks
+  // past nb (a k that is not a multiple of 256) read the next row's codes
+  // and scales, or zero past the planes: every fp16 pattern decodes to a
+  // finite scale, and the activations staged for k past the row are zero,
+  // so those blocks add exact zeros.
+  __device__ __forceinline__ void load(const Planes& P, const Addr& a, int64_t u, int64_t) {
+    const uint32_t sq = static_cast<uint32_t>(u) * 128u, sd = static_cast<uint32_t>(u) * 16u;
     qa = bload16(P.a, a.qa, sq);
     qb = bload16(P.a, a.qb, sq);
-    const uint32_t od = a.d + sd;
-    dl = bload4(P.d, od & ~3u, 0u);
-    dh = bload4(P.d, (od & ~3u) + 4u, 0u);
-    dinfo = static_cast<int32_t>(b + a.dc - nb) * 4 + static_cast<int32_t>(od & 3u);
-  }
-  // d of blocks 8 u + 2 (lane % 4) (bits 0..15) and + 1 (bits 16..31).
-  __device__ __forceinline__ uint32_t d_pair() const {
-    const uint32_t pair = __builtin_amdgcn_alignbyte(dh, dl, static_cast<uint32_t>(dinfo & 3));
-    const int32_t past = dinfo >> 2;  // first block - nb
-    return past >= 0 ? 0u : past == -1 ? pair & 0xffffu : pair;
+    d0 = bload4(P.d, a.d, sd);
+    d1 = bload4(P.d, a.d, sd + 8u);
+    dsh = a.dsh;
   }
   // Once the unit's loads have arrived: qa <- step 0 of all 16 rows (rows
   // 0..7 in lanes 0..31, rows 8..15 in lanes 32..63), qb <- step 1. One
@@ -1118,7 +1128,7 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
   // Piece of step h of the pair for MFMA lane (row lane % 16, group lane / 16)
   // (after arrange()).
   __device__ __forceinline__ void piece(MoePiece<SPIRAL_TYPE_Q4_0>& out, int h, int lane) const {
-    const int r = lane & 15, g = lane >> 4, b = 4 * h + g;
+    const int r = lane & 15, g = lane >> 4;
     const int src = (32 * (r >> 3) + 4 * (r & 7) + g) << 2;
     const uint4 v = h ? qb : qa;
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
@@ -1126,9 +1136,7 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
 #pragma unroll
     for (int j = 0; j < 4; ++j) q[j] = static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute(src, static_cast<int>(vv[j])));
     out.q = make_uint4(q[0], q[1], q[2], q[3]);
-    const uint32_t dv =
-        static_cast<uint32_t>(__builtin_amdgcn_ds_bpermute((32 * h + 2 * r + (g >> 1)) << 2, static_cast<int>(d_pair())));
-    out.d = (b & 1) ? dv >> 16 : dv & 0xffffu;
+    out.d = __builtin_amdgcn_ubfe(h ? d1 : d0, dsh, 16);
   }
 };
 
@@ -1191,7 +1199,7 @@ __device__ __forceinline__ void moe_route(const int32_t* __restrict__ ids, int32
 // of expert e (Z = gridDim.z), so the passes of a heavily routed expert run
 // side by side.
 template <int TYPE, bool F32_OUT, bool GLU, int TB, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES) moe_stream_kernel(
+__global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)) moe_stream_kernel(
     const uint8_t* __restrict__ w, int64_t expert_stride, int64_t n_rows, int64_t k, const uint16_t* __restrict__ x,
     int64_t x_slots, int64_t top_k, const int32_t* __restrict__ ids, int32_t n_pairs, int32_t n_expert,
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
