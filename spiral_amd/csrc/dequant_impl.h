@@ -222,22 +222,20 @@ struct Piece<SPIRAL_TYPE_Q4_0> {
   }
   __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
   // fp16 (1024 + c) times d minus 1032 d is (c - 8) d, exact inside the FMA.
-  // High nibbles are taken in place: byte 16 c is fp16 1024 + 16 c, and
-  // (1024 + 16 c) d / 16 - 72 d is (c - 8) d, exact as well (d / 16 is a
-  // power-of-two scaling of a normal value), with no shift. The scale decode
-  // has no branch, so the compiler can spread this among the MFMAs of the
-  // kernel's step.
+  // High nibbles are taken in place: byte 16 c under the high byte 0x54 is
+  // the fp16 64 + c, and (64 + c) d - 72 d is (c - 8) d, exact as well, with
+  // no shift. The scale decode has no branch, so the compiler can spread
+  // this among the MFMAs of the kernel's step.
   __device__ __forceinline__ void dequant(const Addr& A, uint4& o0, uint4& o1) const {
-    const float m = fp16_scale(d);
-    const float df = A.hi ? 0.0625f * m : m, off = (A.hi ? -72.0f : -1032.0f) * m;
-    const uint32_t mask = A.hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    const float df = fp16_scale(d), off = (A.hi ? -72.0f : -1032.0f) * df;
+    const uint32_t mask = A.hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu, magic = A.hi ? 0x54545454u : 0x64646464u;
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
     uint32_t o[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t c = w[i] & mask;
-      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
-      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04030402u));
       o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), df, off), __builtin_fmaf(static_cast<float>(a.y), df, off));
       o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), df, off), __builtin_fmaf(static_cast<float>(b.y), df, off));
     }

@@ -171,13 +171,13 @@ struct Pipe {
 // Tile (s + 2) % 4 was last read at step s - 2 and tile s % 4 was written at
 // step s - 2, so one barrier after every odd step orders both.
 template <int TYPE>
-__device__ __forceinline__ void gemm_step(f32x4_t (&acc)[4][4], Pipe<TYPE>& pp, uint16_t* bs0, int d, int64_t s,
-                                          int64_t full, __amdgpu_buffer_rsrc_t X, const uint32_t (&voff)[4],
+__device__ __forceinline__ void gemm_step(f32x4_t (&acc)[4][4], Pipe<TYPE>& pp, uint16_t* bs0, int d, int s,
+                                          int full, __amdgpu_buffer_rsrc_t X, const uint32_t (&voff)[4],
                                           const Planes& P, const typename Piece<TYPE>::Addr& pa, int q, int tid,
                                           int lane) {
   constexpr int A = kARing<TYPE>, R = kWRing<TYPE>;
-  load_a(pp.a[(d + A - 1) % A], X, voff, min(s + A - 1, full - 1) * kBK + 32 * q);
-  pp.pc[(d + 1) % R].load(P, pa, min(s + R + 1, full - 1) * kBK);
+  load_a(pp.a[(d + A - 1) % A], X, voff, static_cast<int64_t>(min(s + A - 1, full - 1)) * kBK + 32 * q);
+  pp.pc[(d + 1) % R].load(P, pa, static_cast<int64_t>(min(s + R + 1, full - 1)) * kBK);
   BFrag b;
   read_bfrag(b, bs0 + d * kBTile, q, lane);
   mfma_step(acc, pp.a[d % A], b);
@@ -201,7 +201,9 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const uint8_t* __restric
   const int64_t m0 = (tile / n_tiles_n) * kBM, n0 = (tile % n_tiles_n) * kBN;
   const int64_t row0 = m0 + 64 * mw;
   const int64_t nb = k / block_elems(TYPE);
-  const int64_t full = k / kBK;
+  // 32-bit step counters keep the ring's clamps scalar (k is at most
+  // gemm_max_k(), so k / 128 fits)
+  const int full = static_cast<int>(k / kBK);
   const int tail = static_cast<int>(k - full * kBK);  // 0, 32, 64 or 96
 
   const int64_t kk_n = k >> 5, mb_n = (m + 15) >> 4;
@@ -223,14 +225,14 @@ __global__ void __launch_bounds__(kThreads) gemm_kernel(const uint8_t* __restric
     constexpr int A = kARing<TYPE>, R = kWRing<TYPE>;
     Pipe<TYPE> pp;
 #pragma unroll
-    for (int i = 0; i < A - 1; ++i) load_a(pp.a[i], X, voff, min<int64_t>(i, full - 1) * kBK + 32 * q);
+    for (int i = 0; i < A - 1; ++i) load_a(pp.a[i], X, voff, static_cast<int64_t>(min(i, full - 1)) * kBK + 32 * q);
 #pragma unroll
-    for (int i = 0; i < R; ++i) pp.pc[i].load(P, pa, min<int64_t>(i, full - 1) * kBK);
+    for (int i = 0; i < R; ++i) pp.pc[i].load(P, pa, static_cast<int64_t>(min(i, full - 1)) * kBK);
     store_b<TYPE>(pp.pc[0], pa, Bs, tid);
     store_b<TYPE>(pp.pc[1], pa, Bs + kBTile, tid);
-    pp.pc[0].load(P, pa, min<int64_t>(R, full - 1) * kBK);
+    pp.pc[0].load(P, pa, static_cast<int64_t>(min(R, full - 1)) * kBK);
     __syncthreads();
-    int64_t s0 = 0;
+    int s0 = 0;
     for (; s0 + kRing <= full; s0 += kRing) {
 #pragma unroll
       for (int d = 0; d < kRing; ++d) gemm_step<TYPE>(acc, pp, Bs, d, s0 + d, full, X, voff, P, pa, q, tid, lane);

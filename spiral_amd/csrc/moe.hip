@@ -200,20 +200,20 @@ struct MoePiece;
 
 // Q4_0: piece = block 4 kb + g. MFMA s takes qs dword s: its low nibbles
 // (elements 4s .. 4s + 3) then its high nibbles (16 + 4s .. 16 + 4s + 3).
-// A high nibble c is taken in place (byte 16 c, fp16 1024 + 16 c) against
-// the scale m / 16 and offset -72 m: (1024 + 16 c) m / 16 - 72 m = (c - 8) m,
-// exact inside the FMA as for the low nibbles, with no shift.
+// A high nibble c is taken in place: byte 16 c under the high byte 0x54 is
+// the fp16 64 + c (exponent 6, mantissa step 1/16), and (64 + c) m - 72 m is
+// (c - 8) m, exact inside the FMA as (1024 + c) m - 1032 m is for the low
+// nibbles, with no shift.
 template <>
 struct MoePiece<SPIRAL_TYPE_Q4_0> {
   uint4 q;
   uint32_t d;
-  float m, off, m16, off16;  // decoded scale and offsets (prep)
+  float m, off, off_hi;  // decoded scale and offsets (prep)
   static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
   __device__ __forceinline__ void prep() {
     m = fp16_scale_fma(d);
     off = -1032.0f * m;
-    m16 = 0.0625f * m;
-    off16 = -72.0f * m;
+    off_hi = -72.0f * m;
   }
   // blk = block index of the lane's piece within the row's planar planes
   __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t blk) {
@@ -229,14 +229,14 @@ struct MoePiece<SPIRAL_TYPE_Q4_0> {
     float v[8];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint32_t c = i ? hi : lo;
-      const float df = i ? m16 : m, of = i ? off16 : off;
-      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
-      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
-      v[4 * i] = __builtin_fmaf(static_cast<float>(a.x), df, of);
-      v[4 * i + 1] = __builtin_fmaf(static_cast<float>(a.y), df, of);
-      v[4 * i + 2] = __builtin_fmaf(static_cast<float>(b.x), df, of);
-      v[4 * i + 3] = __builtin_fmaf(static_cast<float>(b.y), df, of);
+      const uint32_t c = i ? hi : lo, magic = i ? 0x54545454u : 0x64646464u;
+      const float of = i ? off_hi : off;
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04030402u));
+      v[4 * i] = __builtin_fmaf(static_cast<float>(a.x), m, of);
+      v[4 * i + 1] = __builtin_fmaf(static_cast<float>(a.y), m, of);
+      v[4 * i + 2] = __builtin_fmaf(static_cast<float>(b.x), m, of);
+      v[4 * i + 3] = __builtin_fmaf(static_cast<float>(b.y), m, of);
     }
     return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
                       pack_bf16x2(v[6], v[7]));
