@@ -741,13 +741,20 @@ int launch_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* 
 // x in LDS (64 bf16 per task) with J = 1, in 16-wave workgroups (x staged
 // once per 16 rows; 5 % faster than 8 waves on the 4096x14336 shape, while
 // deeper rings, two tasks per lane and fewer resident workgroups were slower).
+// Kernels whose registers allow three waves a SIMD but not four (Q8_0 at
+// J = 4, 138 VGPRs; Q5_K at J = 2, 133) run 12-wave workgroups, one a CU,
+// instead of leaving a third of the slots empty: 14336x4096 Q8_0 11.73 us
+// against 11.83 for 8 waves and Q5_K 10.86 against 11.65 (medians), while
+// 4- and 6-wave workgroups and a third ring slot were slower for Q8_0.
+// Those that fit four (Q4_0, Q4_K, IQ4) keep two 8-wave workgroups a CU:
+// 12- and 10-wave ones were 2-20 % slower.
 template <int TYPE>
 int launch_gemv(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   const int64_t T = k / Fmt<TYPE>::kTaskElems;
   if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<TYPE, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
   if (T <= 64) return launch_j<TYPE, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 128) return launch_j<TYPE, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  return launch_j<TYPE, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 128) return launch_j<TYPE, 2, TYPE == SPIRAL_TYPE_Q5_K ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
+  return launch_j<TYPE, 4, 12, 2>(w, n_rows, k, x, y, y_type, s);
 }
 
 }  // namespace
