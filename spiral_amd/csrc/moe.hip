@@ -1084,6 +1084,18 @@ struct Unit<SPIRAL_TYPE_Q4_0> {
   uint32_t dsh;  // 0 or 16
   struct Addr {
     uint32_t qa, qb, d, dsh;
+    // The same lanes `rows` rows further on (rows may be negative). Rows
+    // past the matrix are left past its planes, where the buffer loads
+    // read zero, instead of being clamped to its last row.
+    __device__ __forceinline__ void advance(int64_t rows, int64_t nb) {
+      const int64_t blocks = rows * nb;
+      const uint32_t dq = static_cast<uint32_t>(blocks * 16);
+      qa += dq;
+      qb += dq;
+      const uint32_t od = d + (dsh >> 3) + static_cast<uint32_t>(blocks * 2);  // byte offset of the lane's d
+      d = od & ~3u;
+      dsh = (od & 2u) << 3;
+    }
   };
   static __device__ __forceinline__ Addr addr(int64_t row0, int64_t n_rows, int64_t nb, int lane) {
     Addr a;
@@ -1273,11 +1285,21 @@ __global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)
       ring[slot].load(lu < units ? P : Pu, la, lu < units ? lu : lu - static_cast<int>(units), nb);
       if (++nl < n_units) {
         ++lu;
-        if (GLU && lu == units) la = U::addr(up_row0 + row_of(lj) - (lane & 15), mat_rows, nb, lane);  // up rows
+        // Q4_0 steps its offsets (a few 32-bit adds) where the other
+        // formats recompute them from the row.
+        if (GLU && lu == units) {  // up rows
+          if constexpr (TYPE == SPIRAL_TYPE_Q4_0)
+            la.advance(up_row0, nb);
+          else
+            la = U::addr(up_row0 + row_of(lj) - (lane & 15), mat_rows, nb, lane);
+        }
         if (lu == gunits) {
           lu = 0;
           ++lj;
-          la = U::addr(row_of(lj) - (lane & 15), mat_rows, nb, lane);
+          if constexpr (TYPE == SPIRAL_TYPE_Q4_0)
+            la.advance(16 * WAVES - (GLU ? up_row0 : 0), nb);
+          else
+            la = U::addr(row_of(lj) - (lane & 15), mat_rows, nb, lane);
         }
       }
     };
@@ -1538,7 +1560,11 @@ __global__ void __launch_bounds__(kSkinnyThreads) skinny_kernel(const uint8_t* _
     if (++nl < n_units && ++lu == le) {  // past the last unit the ring re-reads it
       if (!WINDOWS || ++lv == n_win) {
         lv = 0;
-        la = U::addr(row0_of(++lb), n_rows, nb, lane);
+        ++lb;
+        if constexpr (TYPE == SPIRAL_TYPE_Q4_0)
+          la.advance(static_cast<int64_t>(gridDim.x) * per_block * 16, nb);
+        else
+          la = U::addr(row0_of(lb), n_rows, nb, lane);
       }
       lu = slice(lv, part);
       le = slice(lv, part + 1);
