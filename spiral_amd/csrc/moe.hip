@@ -1594,29 +1594,36 @@ __global__ void __launch_bounds__(kSkinnyThreads) skinny_kernel(const uint8_t* _
     // acc: lane l holds x rows 4 (l / 16) + i of weight row row0 + l % 16.
     f32x4_t sum = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     float* rb = red + (cb & 1) * (kSkinnyWaves * 4 * 64);
+    // With k slices (parts > 1), slice 0's wave sums and stores x rows
+    // 4 g + 0, 1 of the group and slice 1's rows 4 g + 2, 3; the other
+    // slices' waves repeat one of the two sums and store nothing. Each sum
+    // adds the slices in slice order, so results do not depend on timing.
+    const int i0 = 2 * (part & 1);
     if (parts > 1) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) rb[(wave * 4 + i) * 64 + lane] = sum[i];
       // every wave is done with this block's partial sums (and with x)
       __syncthreads();
-      // slices in order (every wave adds them; the first slice's wave stores)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sum[i] = rb[(gslot * parts * 4 + i) * 64 + lane];
+      const float* rg = rb + (gslot * parts * 4 + i0) * 64 + lane;
+      float s0 = rg[0], s1 = rg[64];
       for (int p = 1; p < parts; ++p) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sum[i] += rb[((gslot * parts + p) * 4 + i) * 64 + lane];
+        s0 += rg[p * 4 * 64];
+        s1 += rg[p * 4 * 64 + 64];
       }
+      sum = i0 ? f32x4_t{sum[0], sum[1], s0, s1} : f32x4_t{s0, s1, sum[2], sum[3]};
     } else if (WINDOWS && cb + 1 < my_blocks) {
       __syncthreads();  // every wave is done with x
     }
     // Lanes with nothing to store set bit 31 of the offset (past the buffer);
     // bit arithmetic, not a select, so no branch forms around the stores.
     const int64_t n = row0_of(cb) + (lane & 15);
-    const uint32_t skip = static_cast<uint32_t>(part != 0) | static_cast<uint32_t>(n >= n_rows);
+    const uint32_t skip = static_cast<uint32_t>(n >= n_rows);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 4 * g + i;
-      const uint32_t bad = (skip | static_cast<uint32_t>(t >= m)) << 31;
+      const uint32_t mine = static_cast<uint32_t>(parts == 1) | (static_cast<uint32_t>(part < 2) &
+                                                                    static_cast<uint32_t>((i >> 1) == part));
+      const uint32_t bad = (skip | (mine ^ 1u) | static_cast<uint32_t>(t >= m)) << 31;
       const uint32_t off = (static_cast<uint32_t>(min(t, m - 1) * ldy + min(n, n_rows - 1)) * kEsize) | bad;
       if constexpr (F32_OUT)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum[i]), Y, off, 0, 0);
