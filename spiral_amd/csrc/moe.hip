@@ -1703,8 +1703,8 @@ SkinnyShape skinny_shape(int type, int64_t n_rows, int64_t k, int64_t m) {
   if (fit < 1) return sh;
   sh.n_win = static_cast<int>(ceil_div(sh.units, fit));
   sh.win_units = ceil_div(sh.units, sh.n_win);
-  // As many slices as the windows allow (up to one wave per slice): the
-  // finest blocks, so the persistent grid divides the work evenly.
+  // The most slices the windows allow (up to one wave per slice); the
+  // launch picks among the powers of two up to it (skinny_parts).
   const int64_t min_win = sh.units / sh.n_win;
   int parts = 1;
   while (parts < kSkinnyWaves && 2 * parts <= min_win) parts *= 2;
@@ -1713,19 +1713,44 @@ SkinnyShape skinny_shape(int type, int64_t n_rows, int64_t k, int64_t m) {
   return sh;
 }
 
+// k slices per 16-row group for `resident` workgroups at once. sh.parts is
+// the most the windows allow; a launch takes the count that gives the
+// busiest wave the fewest units, and among those the fewest block ends (a
+// block end is an LDS exchange of partial sums behind a barrier, about
+// 0.6 us at m = 4 on 14336 x 4096 Q4_0: 8 slices (four blocks a workgroup)
+// took 15.8 us, 4 slices 14.3 and 2 slices (one block) 13.9, every choice
+// giving the busiest wave 8 units).
+int skinny_parts(const SkinnyShape& sh, int64_t resident) {
+  int best = sh.parts;
+  int64_t best_units = INT64_MAX, best_ends = INT64_MAX;
+  for (int p = 1; p <= sh.parts; p *= 2) {
+    const int64_t n_blocks = ceil_div(sh.groups, kSkinnyWaves / p);
+    const int64_t wgs = std::min(n_blocks, std::max<int64_t>(1, resident));
+    const int64_t ends = ceil_div(n_blocks, wgs);             // blocks of the busiest workgroup
+    const int64_t units = ends * sh.n_win * ceil_div(sh.win_units, p);  // its waves' units, at most
+    if (units < best_units || (units == best_units && ends < best_ends)) {
+      best = p;
+      best_units = units;
+      best_ends = ends;
+    }
+  }
+  return best;
+}
+
 template <int TYPE, bool F32_OUT, bool WINDOWS>
 int launch_skinny(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
                   int64_t ldy, const SkinnyShape& sh, hipStream_t s) {
   const auto kern = skinny_kernel<TYPE, F32_OUT, WINDOWS>;
   const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), static_cast<int>(kSkinnyLds));
   if (rc != SPIRAL_OK) return rc;
-  const int64_t n_blocks = ceil_div(sh.groups, kSkinnyWaves / sh.parts);
   const int64_t resident =
       static_cast<int64_t>(device_cu_count()) * blocks_per_cu(reinterpret_cast<const void*>(kern), kSkinnyThreads, sh.lds);
+  const int parts = skinny_parts(sh, resident);
+  const int64_t n_blocks = ceil_div(sh.groups, kSkinnyWaves / parts);
   const int pitch = static_cast<int>(128 * Unit<TYPE>::kSteps * sh.win_units + kAPad);
   const dim3 grid(static_cast<unsigned>(std::min(n_blocks, resident)));
   hipLaunchKernelGGL(kern, grid, dim3(kSkinnyThreads), static_cast<size_t>(sh.lds), s,
-                     static_cast<const uint8_t*>(w), n_rows, k, x, ldx, static_cast<int>(m), y, ldy, sh.parts,
+                     static_cast<const uint8_t*>(w), n_rows, k, x, ldx, static_cast<int>(m), y, ldy, parts,
                      sh.n_win, pitch);
   return launch_status();
 }
