@@ -66,41 +66,21 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t grid) {
 }
 
 // Xp[mb][kk][lane][8] = X[16 mb + lane % 16][32 kk + 8 (lane / 16) + e];
-// rows past m are zero. Workgroup (mb, group of 16 kk) packs a 16-row x
-// 512-column tile through LDS:
-//  - wave w reads rows 4 w .. + 3 of the tile, each as one 1 KiB load with
-//    consecutive lanes on consecutive 16 bytes of the row (reading the
-//    fragments straight from X puts consecutive lanes on different rows,
-//    which the gfx950 address path serves at about a third of the rate);
-//  - after a barrier, wave w writes fragments kk = 16 g + 4 w .. + 3, each a
-//    1 KiB store of consecutive bytes. Tile rows are padded by 16 bytes so
-//    the 16 rows a fragment reads land in different LDS banks.
-constexpr int kPackPitch = 512 + 8;  // bf16 per LDS tile row
+// rows past m are zero. Wave w of the grid writes fragment f = w (1 KiB of
+// consecutive bytes, one store); its lanes read their 16 bytes straight from
+// X. The pass moves 2 x 4 MiB at m = 512, k = 4096, so the latency of one
+// load and one store per lane is what it costs: no LDS tile, no barrier.
 __global__ void __launch_bounds__(256) pack_x_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t m,
                                                      int64_t k, uint16_t* __restrict__ xp) {
-  __shared__ __align__(16) uint16_t tile[16 * kPackPitch];
   const uint32_t kk_n = static_cast<uint32_t>(k >> 5);
-  const uint32_t groups = (kk_n + 15) >> 4;
-  const uint32_t mb = blockIdx.x / groups, kg = blockIdx.x - mb * groups;
-  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-  const int64_t col = 512 * static_cast<int64_t>(kg) + 8 * lane;  // this lane's 8 columns
-  uint4 v[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int64_t r = 16 * static_cast<int64_t>(mb) + 4 * w + t;
-    v[t] = make_uint4(0u, 0u, 0u, 0u);
-    if (r < m && col < k) v[t] = *reinterpret_cast<const uint4*>(x + r * ldx + col);
-  }
-#pragma unroll
-  for (int t = 0; t < 4; ++t) *reinterpret_cast<uint4*>(tile + (4 * w + t) * kPackPitch + 8 * lane) = v[t];
-  __syncthreads();
-  const uint32_t kk0 = 16 * kg + 4 * w;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    if (kk0 + t >= kk_n) break;
-    const uint4 f = *reinterpret_cast<const uint4*>(tile + (lane & 15) * kPackPitch + 32 * (4 * w + t) + 8 * (lane >> 4));
-    *reinterpret_cast<uint4*>(xp + ((static_cast<int64_t>(mb) * kk_n + kk0 + t) * 64 + lane) * 8) = f;
-  }
+  const uint32_t frags = static_cast<uint32_t>((m + 15) >> 4) * kk_n;
+  const uint32_t f = blockIdx.x * 4u + (threadIdx.x >> 6), lane = threadIdx.x & 63u;
+  if (f >= frags) return;
+  const uint32_t mb = f / kk_n, kk = f - mb * kk_n;
+  const int64_t r = 16 * static_cast<int64_t>(mb) + (lane & 15u);
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (r < m) v = *reinterpret_cast<const uint4*>(x + r * ldx + 32 * kk + 8 * (lane >> 4));
+  *reinterpret_cast<uint4*>(xp + (static_cast<int64_t>(f) * 64 + lane) * 8) = v;
 }
 
 // The four X fragments (m-blocks) of a wave for one k-quarter.
@@ -343,7 +323,7 @@ int launch_gemm(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int
   for (int64_t mo = 0; mo < m; mo += chunk) {
     const int64_t mc = std::min(chunk, m - mo);
     const int64_t tm = ceil_div(mc, kBM);
-    const int64_t packs = ceil_div(mc, 16) * ceil_div(k >> 5, 16);
+    const int64_t packs = ceil_div(ceil_div(mc, 16) * (k >> 5), 4);
     if (tn * tm > INT32_MAX || packs > INT32_MAX) return SPIRAL_ERR_SHAPE;
     hipLaunchKernelGGL(pack_x_kernel, dim3(static_cast<unsigned>(packs)), dim3(256), 0, s, x + mo * ldx, ldx, mc, k,
                        xp);
