@@ -5,12 +5,13 @@
     python bench.py --write-traffic DIR   (DIR: rocprofv3 --pmc csv output, see below)
 
 Headline (the JSON line's "value"): Q8_0 decode GEMV y[14336] = W[14336 x 4096]
-x[4096], batch 1 -- packed-weight GB/s. The same line carries the other
+x[4096], batch 1 -- packed-weight GB/s -- with exact bf16 weights (the
+default product). The same line carries the other
 workloads under "workloads": Q4_0 GEMV (14336 x 4096), the Q4_0 small-batch
 product at m = 4 (same matrix), Q4_0 -> bf16 dequant (4096 x 4096), Q6_K GEMV
 and Q6_K -> bf16 dequant (4096 x 14336), Q4_0 dequant-GEMM (M = 512, N = K = 4096), the Q4_0 MoE
 grouped GEMM (128 experts, 64 tokens, top-8) and its gate_up stage fused with
-SwiGLU.
+SwiGLU, and the Q8_0 GEMV in the named relaxed mode (gemv_relaxed_q8_0).
 
 Measurement
   - Inputs are synthetic and seeded, converted to the planar layout and
@@ -38,8 +39,9 @@ Measurement
     DIR rebuilds that file from DIR/{bench,copy}_{FETCH,WRITE}_SIZE/
     p_counter_collection.csv (rocprofv3 --pmc X --output-format csv -o p
     over this script, and over this script with --copy-calibration).
-  - "cpu_baseline" (the headline's, and one in each of the Q8_0 GEMV, Q4_0
-    dequant and Q4_0 GEMM workloads): oracle/cpu_baseline.c over the same
+  - "cpu_baseline" (the headline's, and one in each of the Q8_0 and Q6_K GEMV,
+    Q4_0 and Q6_K dequant, Q4_0 GEMM and Q4_0 MoE workloads):
+    oracle/cpu_baseline.c over the same
     canonical tensors -- the reference's CPU semantics, vectorized (AVX-512 /
     AVX2 clones picked at load) and spread over min(16, usable) host threads --
     repeated for --cpu-seconds split across the legs; each records nproc,
@@ -104,6 +106,8 @@ class Timer:
         self.replays = replays
         self.spread = []
         self.preroll = 0.0
+        self.late = False  # the last run's window still held host issue time
+        self.timed_late = False  # the same, for the timed run
         self._cps = None
 
     def _cycles_per_s(self):
@@ -141,6 +145,7 @@ class Timer:
                 break
             preroll_s *= 2
         self.preroll = preroll_s  # later runs start from the length that sufficed
+        self.late = late
         return issue, start.elapsed_time(end) * 1e-3
 
     def run(self, launch, steps, warmup):
@@ -156,6 +161,7 @@ class Timer:
         self.preroll = min(0.05, 2.0 * issue + 2e-4)
         self._timed(launch, steps, self.preroll)  # untimed: the same sequence once, clocks settling
         _, ev = self._timed(launch, steps, self.preroll)
+        self.timed_late = self.late
         self.spread = [self._timed(launch, steps, self.preroll)[1] / steps for _ in range(self.replays)]
         return issue, ev
 
@@ -173,13 +179,15 @@ def traffic_table():
 # workload -> (kernel-name fragments whose dispatches make one step, algorithmic
 # bytes of one step or None)
 TRAFFIC_KERNELS = {
-    "gemv_q8_0": (["gemv_kernel<8,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
-    "gemv_q6_k": (["gemv_kernel<14,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
-    "gemv_q4_0": (["gemv_kernel<2,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
-    "gemv_q4_k": (["gemv_kernel<12,"], 14336 * 4096 // 256 * 144 + 4096 * 2 + 14336 * 2),
-    "gemv_q5_k": (["gemv_kernel<13,"], 14336 * 4096 // 256 * 176 + 4096 * 2 + 14336 * 2),
-    "gemv_iq4_nl": (["gemv_kernel<20,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
-    "gemv_iq4_xs": (["gemv_kernel<23,"], 14336 * 4096 // 256 * 136 + 4096 * 2 + 14336 * 2),
+    "gemv_q8_0": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<8>,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
+    "gemv_q6_k": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<14>,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
+    "gemv_q4_0": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<2>,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "gemv_q4_k": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<12>,"], 14336 * 4096 // 256 * 144 + 4096 * 2 + 14336 * 2),
+    "gemv_q5_k": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<13>,"], 14336 * 4096 // 256 * 176 + 4096 * 2 + 14336 * 2),
+    "gemv_iq4_nl": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<20>,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "gemv_iq4_xs": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<23>,"], 14336 * 4096 // 256 * 136 + 4096 * 2 + 14336 * 2),
+    "gemv_relaxed_q8_0": (["gemv_kernel<spiral::(anonymousnamespace)::Fmt<8>,"],
+                          14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
     "mul_mat_q4_0_m4": (["skinny_kernel<2,"], 14336 * 4096 // 32 * 18 + 4 * 4096 * 2 + 4 * 14336 * 2),
     "dequant_q4_0": (["dequant_kernel<2>"], 4096 * 4096 // 32 * 18 + 4096 * 4096 * 2),
     "dequant_q6_k": (["dequant_kernel<14>"], 4096 * 14336 // 256 * 210 + 4096 * 14336 * 2),
@@ -257,7 +265,8 @@ def cpu_legs(args, results, inputs):
     from oracle import oracle as O
     host = O.host_cpu()
     threads = min(16, host["affinity"] or 1)  # the GPU box's CPU share is 16 cores
-    legs = [n for n in ("gemv_q8_0", "dequant_q4_0", "gemm_q4_0") if n in inputs and n in results]
+    legs = [n for n in ("gemv_q8_0", "gemv_q6_k", "dequant_q4_0", "dequant_q6_k", "gemm_q4_0", "moe_q4_0")
+            if n in inputs and n in results]
     budget = args.cpu_seconds / max(1, len(legs))
 
     def timed(fn):
@@ -277,6 +286,12 @@ def cpu_legs(args, results, inputs):
             base.update(value=raw.size * p / dt / 1e9, unit="GB/s",
                         sample=f"{p} passes of the Q8_0 14336x4096 GEMV (canonical GGUF bytes, packed-weight GB/s), "
                                f"{dt:.1f} s")
+        elif name == "gemv_q6_k":
+            raw, x = inputs[name]
+            p, dt = timed(lambda: O.cb_gemv_q6_k(raw, 4096, 14336, x, threads))
+            base.update(value=raw.size * p / dt / 1e9, unit="GB/s",
+                        sample=f"{p} passes of the Q6_K 4096x14336 GEMV (canonical GGUF bytes, packed-weight GB/s), "
+                               f"{dt:.1f} s")
         elif name == "dequant_q4_0":
             (raw,) = inputs[name]
             out = np.empty((4096, 4096), dtype=np.uint16)
@@ -284,11 +299,31 @@ def cpu_legs(args, results, inputs):
             base.update(value=(raw.size + out.nbytes) * p / dt / 1e9, unit="GB/s",
                         packed_GBps=raw.size * p / dt / 1e9,
                         sample=f"{p} passes of the Q4_0 4096x4096 -> bf16 dequant (bytes in + out), {dt:.1f} s")
-        else:
+        elif name == "dequant_q6_k":
+            (raw,) = inputs[name]
+            out = np.empty((4096, 14336), dtype=np.uint16)
+            p, dt = timed(lambda: O.cb_dequant_q6_k(raw, 4096, 14336, threads, out))
+            base.update(value=(raw.size + out.nbytes) * p / dt / 1e9, unit="GB/s",
+                        packed_GBps=raw.size * p / dt / 1e9,
+                        sample=f"{p} passes of the Q6_K 4096x14336 -> bf16 dequant (bytes in + out), {dt:.1f} s")
+        elif name == "gemm_q4_0":
             raw, x = inputs[name]
             p, dt = timed(lambda: O.cb_gemm_q4_0(raw, 4096, 4096, x, threads))
             base.update(value=2.0 * 512 * 4096 * 4096 * p / dt / 1e9, unit="GFLOP/s",
                         sample=f"{p} passes of the Q4_0 GEMM Y[512x4096] = X W^T, {dt:.1f} s")
+        else:
+            gu_raw, dn_raw, ids, x1, x2 = inputs[name]
+            gu_per, dn_per = gu_raw.size // 128, dn_raw.size // 128
+
+            def step():
+                O.cb_moe_q4_0(gu_raw, gu_per, 128, 1536, 2048, x1, ids, threads)
+                O.cb_moe_q4_0(dn_raw, dn_per, 128, 2048, 768, x2, ids, threads)
+
+            p, dt = timed(step)
+            touched = np.unique(ids).size
+            base.update(value=touched * (gu_per + dn_per) * p / dt / 1e9, unit="GB/s",
+                        sample=f"{p} steps of the Q4_0 MoE (gate_up + down MUL_MAT_ID over 128 experts, 64 tokens, "
+                               f"top-8; touched experts' packed bytes), {dt:.1f} s")
         r = results[name]
         gpu = r["value"] * (1e3 if r["unit"] == "TFLOP/s" else 1.0)
         base["gpu_over_cpu"] = gpu / base["value"]
@@ -339,6 +374,7 @@ def main():
         achieved = per_launch / step / scale
         r = {"value": per_launch * steps / ev / scale, "unit": unit, "ms_per_step": step * 1e3,
              "issue_us_per_step": issue / steps * 1e6, "step_us": step * 1e6,
+             "preroll_ms": timer.preroll * 1e3, "late": bool(timer.timed_late),
              "roofline": {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
                           "frac": achieved / peak}}
         if timer.spread:
@@ -364,14 +400,31 @@ def main():
                {"workload": "Q8_0 decode GEMV y[14336] = W[14336x4096] x[4096], batch 1, bf16 out",
                 "bytes_per_launch": wbytes, "copies": len(ws)})
         cpu_inputs["gemv_q8_0"] = (raw, x)
+        # the named relaxed mode on the same weights (block scale after the
+        # block sum, weights not rounded to bf16): not the headline
+        del ws
+
+    if want("gemv_relaxed_q8_0"):
+        n, k = 14336, 4096
+        wbytes = n * row_bytes(TYPE_Q8_0, k)
+        _, ws = upload_planar(TYPE_Q8_0, n, k, 1, copies_for(wbytes))
+        _, xd = x_dev(1, k, 2)
+        y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
+        issue, ev = timer.run(lambda i: ops.gemv_relaxed(TYPE_Q8_0, ws[i % len(ws)], n, k, xd, out=y), steps,
+                              warmup)
+        record("gemv_relaxed_q8_0", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
+               {"workload": "Q8_0 decode GEMV 14336x4096, batch 1, bf16 out, in the named relaxed mode "
+                            "(spiral_gemv_relaxed: block scale after the block sum; not the exact default)",
+                "bytes_per_launch": wbytes, "copies": len(ws)})
         del ws
 
     # --- Q6_K GEMV ------------------------------------------------------------
     if want("gemv_q6_k"):
         n, k = 4096, 14336
         wbytes = n * row_bytes(TYPE_Q6_K, k)
-        _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies_for(wbytes))
-        _, xd = x_dev(1, k, 4)
+        raw6, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies_for(wbytes))
+        x6, xd = x_dev(1, k, 4)
+        cpu_inputs["gemv_q6_k"] = (raw6, x6)
         y = torch.empty((1, n), dtype=torch.bfloat16, device=dev)
         issue, ev = timer.run(lambda i: ops.mul_mat(TYPE_Q6_K, ws[i % len(ws)], n, k, xd, out=y), steps, warmup)
         record("gemv_q6_k", issue, ev, wbytes, "GB/s", HBM_PEAK_GBS, "hbm",
@@ -446,7 +499,8 @@ def main():
         inb = n * row_bytes(TYPE_Q6_K, k)
         outb = n * k * 2
         copies = copies_for(inb + outb)
-        _, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies)
+        raw6, ws = upload_planar(TYPE_Q6_K, n, k, 3, copies)
+        cpu_inputs["dequant_q6_k"] = (raw6,)
         outs = [torch.empty((n, k), dtype=torch.bfloat16, device=dev) for _ in range(copies)]
         issue, ev = timer.run(lambda i: ops.dequant(TYPE_Q6_K, ws[i % copies], n, k, out=outs[i % copies]),
                                steps, warmup)
@@ -491,18 +545,21 @@ def main():
             # every expert generated on its own (seed * 1000 + e), as the Q4_0
             # workload defines a weight; the copies repeat the stack
             first = torch.empty(n_expert * per, dtype=torch.uint8, device=dev)
+            canon = np.empty(n_expert * per, dtype=np.uint8)  # canonical bytes, for the CPU leg
             for e in range(n_expert):
                 raw = synth.make_weights(TYPE_Q4_0, n, k, seed * 1000 + e)
+                canon[e * per:(e + 1) * per] = raw
                 first[e * per:(e + 1) * per] = ops.to_planar(TYPE_Q4_0, torch.from_numpy(raw).to(dev), n, k)
-            return [first] + [first.clone() for _ in range(copies - 1)]
+            return canon, [first] + [first.clone() for _ in range(copies - 1)]
 
-        gus = stacked(inter2, hidden, gu_per, 10)
-        dns = stacked(hidden, inter, dn_per, 11)
+        gu_raw, gus = stacked(inter2, hidden, gu_per, 10)
+        dn_raw, dns = stacked(hidden, inter, dn_per, 11)
         ids_d = torch.from_numpy(ids).to(dev)
-        _, x1 = x_dev(n_tokens, hidden, 12)
+        x1h, x1 = x_dev(n_tokens, hidden, 12)
         x1 = x1.view(n_tokens, 1, hidden)
-        _, x2 = x_dev(n_tokens * top_k, inter, 13)
+        x2h, x2 = x_dev(n_tokens * top_k, inter, 13)
         x2 = x2.view(n_tokens, top_k, inter)
+        cpu_inputs["moe_q4_0"] = (gu_raw, dn_raw, ids, x1h, x2h)
         y1 = torch.empty((n_tokens, top_k, inter2), dtype=torch.bfloat16, device=dev)
         y2 = torch.empty((n_tokens, top_k, hidden), dtype=torch.bfloat16, device=dev)
         ws1 = ops.mul_mat_id_workspace(n_expert, n_tokens, top_k, dev)

@@ -179,7 +179,11 @@ int spiral_get_rows(int type, const void* w, int64_t n_rows, int64_t k,
 
 /* ggml MUL_MAT with quantized src0: y[i][n] = sum_k x[i][k] * W[n][k] for
  * i < m, x bf16 rows of stride ldx elements, y (BF16 or F32) rows of stride ldy
- * elements. fp32 accumulation. m == 1 runs the streaming GEMV; 2 <= m <= 16
+ * elements. Every W[n][k] is the exact dequantized bf16 weight (the value
+ * spiral_dequant_bf16 gives), multiplied by x with fp32 accumulation, as in
+ * the reference's fused dequant + mmul (src/quants/q4_0/mmul.aie.h:16-90,
+ * src/quants/common/mmul.aie.h:9-22); the form chosen for m only changes
+ * the summation order. m == 1 runs the streaming GEMV; 2 <= m <= 16
  * (decode batches, speculative decoding) runs the weight-streaming MFMA form,
  * which reads every weight byte once; larger m runs the MFMA dequant-GEMM,
  * which first rewrites x into MFMA operand order in `workspace` (device
@@ -194,6 +198,22 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k,
                    const uint16_t* x, int64_t ldx, int64_t m, void* y,
                    int y_type, int64_t ldy, void* workspace,
                    int64_t workspace_bytes, void* stream);
+
+/* Named relaxed mode of the single-row product (m = 1), kept apart from the
+ * exact default as the reference requires of fast variants ("separate named
+ * variants with explicit verification policies", src/quants/TODO.md:132-135).
+ * y[n] = sum over blocks of scale * (sum_k code[n][k] * x[k]): the block
+ * scale multiplies the block's fp32 sum, so weights are never rounded to
+ * bf16. That is the scale-after-mmul arithmetic the reference rejects as a
+ * default (src/quants/NOTES.md:327-330). Tolerance, stated and tested:
+ * within 1e-4 (F32 out) of the float64 product over unrounded weights
+ * code * scale; against the exact bf16-weight product it moves outputs by
+ * about 1e-2 of the largest output at k = 4096..14336, so it is tested only
+ * to 2e-2 there. x bf16 [k], y [n_rows] of y_type (BF16 or F32); k at most
+ * spiral_gemv_relaxed_max_k(type) (0 for a type it does not take). */
+int64_t spiral_gemv_relaxed_max_k(int type);
+int spiral_gemv_relaxed(int type, const void* w, int64_t n_rows, int64_t k,
+                        const uint16_t* x, void* y, int y_type, void* stream);
 
 /* ggml MUL_MAT_ID with quantized, expert-stacked src0: for token t < n_tokens
  * and slot s < top_k, y[t][s][:] = W[ids[t][s]] * x[t][s % x_slots][:].

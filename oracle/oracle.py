@@ -302,6 +302,12 @@ def cpu_baseline():
         L.cb_dequant_q4_0.restype = ctypes.c_int
         L.cb_gemm_q4_0.argtypes = [_p, _i64, _i64, _p, _i64, _p, ctypes.c_int]
         L.cb_gemm_q4_0.restype = ctypes.c_int
+        L.cb_gemv_q6_k.argtypes = [_p, _i64, _i64, _p, _p, ctypes.c_int]
+        L.cb_gemv_q6_k.restype = ctypes.c_int
+        L.cb_dequant_q6_k.argtypes = [_p, _i64, _i64, _p, ctypes.c_int]
+        L.cb_dequant_q6_k.restype = ctypes.c_int
+        L.cb_moe_q4_0.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, ctypes.c_int]
+        L.cb_moe_q4_0.restype = ctypes.c_int
         _cb = L
     return _cb
 
@@ -329,6 +335,38 @@ def cb_gemm_q4_0(raw, n_rows, k, x_bf16, threads):
     y = np.empty((x.shape[0], n_rows), dtype=np.float32)
     if cpu_baseline().cb_gemm_q4_0(_ptr(raw), n_rows, k, _ptr(x), x.shape[0], _ptr(y), threads) != 0:
         raise ValueError("cb_gemm_q4_0: bad shape")
+    return y
+
+
+def cb_gemv_q6_k(raw, n_rows, k, x_bf16, threads):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).reshape(-1)
+    y = np.empty(n_rows, dtype=np.float32)
+    if cpu_baseline().cb_gemv_q6_k(_ptr(raw), n_rows, k, _ptr(x), _ptr(y), threads) != 0:
+        raise ValueError("cb_gemv_q6_k: bad shape")
+    return y
+
+
+def cb_dequant_q6_k(raw, n_rows, k, threads, out=None):
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty((n_rows, k), dtype=np.uint16) if out is None else out
+    if cpu_baseline().cb_dequant_q6_k(_ptr(raw), n_rows, k, _ptr(out), threads) != 0:
+        raise ValueError("cb_dequant_q6_k: bad shape")
+    return out
+
+
+def cb_moe_q4_0(raw, expert_bytes, n_expert, n_rows, k, x_bf16, ids, threads):
+    """MUL_MAT_ID over canonical Q4_0 experts stacked at expert_bytes: x is
+    [n_tokens][x_slots][k] bf16 bits, ids [n_tokens][top_k] int32; returns
+    y [n_tokens][top_k][n_rows] float32."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    n_tokens, top_k = ids.shape
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16).reshape(n_tokens, -1, k)
+    y = np.empty((n_tokens, top_k, n_rows), dtype=np.float32)
+    if cpu_baseline().cb_moe_q4_0(_ptr(raw), expert_bytes, n_expert, n_rows, k, _ptr(x), x.shape[1], _ptr(ids),
+                                  n_tokens, top_k, _ptr(y), threads) != 0:
+        raise ValueError("cb_moe_q4_0: bad shape")
     return y
 
 

@@ -52,6 +52,8 @@ SIGNATURES = {
     "spiral_get_rows": (_int, [_int, _p, _i64, _i64, _p, _i64, _p, _int, _i64, _p]),
     "spiral_mul_mat_workspace_bytes": (_i64, [_int, _i64, _i64, _i64]),
     "spiral_mul_mat": (_int, [_int, _p, _i64, _i64, _p, _i64, _i64, _p, _int, _i64, _p, _i64, _p]),
+    "spiral_gemv_relaxed_max_k": (_i64, [_int]),
+    "spiral_gemv_relaxed": (_int, [_int, _p, _i64, _i64, _p, _p, _int, _p]),
     "spiral_mul_mat_id_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "spiral_mul_mat_id": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,
                                  _p, _i64, _p]),

@@ -4,8 +4,8 @@
 #include "common.h"
 
 namespace spiral {
-int64_t gemv_max_k(int type);
-int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
+int64_t gemv_max_k(int type, bool exact);
+int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, bool exact,
          hipStream_t s);
 int64_t gemm_workspace_bytes(int64_t m, int64_t k);
 int64_t gemm_max_k();
@@ -60,7 +60,7 @@ extern "C" {
 
 int64_t spiral_mul_mat_workspace_bytes(int type, int64_t n_rows, int64_t k, int64_t m) {
   if (!is_quant_type(type) || n_rows <= 0 || m <= 0 || k <= 0 || k % block_elems(type) != 0) return 0;
-  if (m == 1 && k <= gemv_max_k(type)) return 0;
+  if (m == 1 && k <= gemv_max_k(type, true)) return 0;
   if (skinny_fits(type, n_rows, k, m)) return 0;
   return gemm_workspace_bytes(m, k);  // 0 past the GEMM's longest row: spiral_mul_mat refuses that shape
 }
@@ -75,7 +75,7 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uin
   if (ldx < k || ldy < n_rows || spiral_tensor_bytes(type, n_rows, k) == 0) return SPIRAL_ERR_SHAPE;
   if (!aligned16(w) || !aligned16(x) || ldx % 8 != 0) return SPIRAL_ERR_ALIGN;
   if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0) return SPIRAL_ERR_ALIGN;
-  const bool direct = (m == 1 && k <= gemv_max_k(type)) || skinny_fits(type, n_rows, k, m);
+  const bool direct = (m == 1 && k <= gemv_max_k(type, true)) || skinny_fits(type, n_rows, k, m);
   if (!direct && k > gemm_max_k()) return SPIRAL_ERR_SHAPE;
   const int64_t need = spiral_mul_mat_workspace_bytes(type, n_rows, k, m);
   if (need > 0) {
@@ -87,10 +87,26 @@ int spiral_mul_mat(int type, const void* w, int64_t n_rows, int64_t k, const uin
   if (rc != SPIRAL_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (direct) {
-    if (m == 1 && k <= gemv_max_k(type)) return gemv(type, w, n_rows, k, x, y, y_type, s);
+    if (m == 1 && k <= gemv_max_k(type, true)) return gemv(type, w, n_rows, k, x, y, y_type, true, s);
     return skinny(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, s);
   }
   return gemm(type, w, n_rows, k, x, ldx, m, y, y_type, ldy, workspace, s);
+}
+
+int64_t spiral_gemv_relaxed_max_k(int type) { return is_quant_type(type) ? gemv_max_k(type, false) : 0; }
+
+int spiral_gemv_relaxed(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
+                        void* stream) {
+  if (!is_quant_type(type)) return SPIRAL_ERR_TYPE;
+  if (y_type != SPIRAL_TYPE_BF16 && y_type != SPIRAL_TYPE_F32) return SPIRAL_ERR_TYPE;
+  if (w == nullptr || x == nullptr || y == nullptr) return SPIRAL_ERR_NULL;
+  if (n_rows <= 0 || k <= 0 || k % block_elems(type) != 0 || k > gemv_max_k(type, false)) return SPIRAL_ERR_SHAPE;
+  if (spiral_tensor_bytes(type, n_rows, k) == 0) return SPIRAL_ERR_SHAPE;
+  if (!aligned16(w) || !aligned16(x)) return SPIRAL_ERR_ALIGN;
+  if ((reinterpret_cast<uintptr_t>(y) & 3u) != 0) return SPIRAL_ERR_ALIGN;
+  const int rc = require_device();
+  if (rc != SPIRAL_OK) return rc;
+  return gemv(type, w, n_rows, k, x, y, y_type, false, static_cast<hipStream_t>(stream));
 }
 
 int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens, int64_t top_k) {

@@ -30,21 +30,31 @@
 //  - A row's fp32 partial sums are reduced across the wave after its last
 //    pass with DPP (six adds, the total in lane 63) and lane 63 stores y.
 //
-// Arithmetic (fp32 accumulation throughout):
-//  - Codes are turned into small floats with an exact offset and the offset
-//    is removed once per task with a precomputed sum of x over the task:
+// Arithmetic (fp32 accumulation throughout). Two modes share the kernel:
+//  - Exact (the default, Exact<TYPE>): every weight is the dequantized bf16
+//    value, bf16_rne(code * scale), the weight the reference's fused product
+//    multiplies (src/quants/q8_0/mmul.aie.h:16-117 dequantizes each tile
+//    before its mmul), and the same weight the small-batch, GEMM and MoE
+//    kernels use, so a row's output does not depend on the batch it is
+//    decoded in. Codes become fp16 pairs with one v_perm_b32 (a byte under
+//    a fixed high byte), v_fma_mix_f32 forms code * scale exactly in fp32
+//    ((B + code) * s - B * s with both terms exact, or a subnormal fp16
+//    code against s * 2^24), v_cvt_pk_bf16_f32 rounds two of them to
+//    nearest even, and v_dot2_f32_bf16 multiplies the pair against a bf16
+//    x pair.
+//  - Relaxed (Fmt<TYPE>, the spiral_gemv_relaxed entry point): the block
+//    scale multiplies the block's fp32 sum, so codes are never rounded to
+//    bf16 weights. That is the scale-after-mmul arithmetic the reference
+//    keeps out of its exact tolerance (src/quants/NOTES.md:327-330) and
+//    allows only as a named mode with its own check
+//    (src/quants/TODO.md:132-135). Codes are turned into small floats with
+//    an exact offset removed once per task with a precomputed sum of x:
 //      sum (q - c) x = sum (q + B) x - (B + c) * sum x.
-//  - Q4_0 and Q6_K form their codes bytewise (nibble masks; Q6_K adds the
-//    two high bits), then bf16 pairs (128 + code) of consecutive elements
-//    with one v_perm_b32 each (code byte low, 0x43 high), and multiply them
-//    against bf16 x pairs with v_dot2_f32_bf16. x is staged unchanged.
-//  - Q8_0 codes (q + 128 up to 255) do not fit a bf16 mantissa; it builds
-//    fp16 pairs (1024 + q + 128) with one v_perm_b32 each (0x64 high) and
-//    multiplies each half against fp32 x with v_fma_mix_f32 (the fp16
-//    operand is widened exactly inside the FMA).
-//  - Weights are not rounded to bf16 first (the block scale multiplies the
-//    block sum), so results differ from the bf16-weight product by rounding
-//    only; tests bound that difference.
+//    Q4_0 and Q6_K form bf16 pairs (128 + code) with one v_perm_b32 each
+//    and multiply them against bf16 x pairs with v_dot2_f32_bf16; Q8_0 codes
+//    (q + 128 up to 255) do not fit a bf16 mantissa, so it builds fp16 pairs
+//    (1024 + q + 128) and multiplies each half against fp32 x with
+//    v_fma_mix_f32.
 #include <algorithm>
 
 #include "common.h"
@@ -83,6 +93,24 @@ __device__ __forceinline__ uint32_t bf16_23(uint32_t w) { return __builtin_amdgc
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
+
+// Two exact weights as a bf16 pair: the bytes of w picked by SEL under the
+// high byte HI form an fp16 pair h (v_perm_b32); each half becomes
+// h * s + c in one v_fma_mix_f32 (the fp16 operand is widened exactly) and
+// the two sums are rounded to nearest even into one bf16 pair. Callers pick
+// HI, s and c so that h * s + c is the exact code * scale.
+template <uint32_t HI, uint32_t SEL>
+__device__ __forceinline__ uint32_t wpair(uint32_t w, float s, float c) {
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(HI, w, SEL));
+  return pack_bf16x2(__builtin_fmaf(static_cast<float>(h.x), s, c), __builtin_fmaf(static_cast<float>(h.y), s, c));
+}
+// Byte selectors: bytes 0 and 1, or 2 and 3, of w into the low bytes of the
+// two halves, the high bytes from HI.
+constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
+// High bytes: 0x64 makes the fp16 1024 + b (exponent 10, step 1), 0x54 makes
+// 64 + b / 16 (exponent 6, step 1/16), 0x00 the subnormal b * 2^-24.
+constexpr uint32_t kHi1024 = 0x64646464u, kHi64 = 0x54545454u, kHiSub = 0u;
+constexpr float kTwo24 = 16777216.0f;
 
 // Blocked LDS layout (see the header): byte offset of entry 0 of task t when
 // a task has E 16-byte entries; entry e adds e KiB.
@@ -596,19 +624,216 @@ struct Fmt<SPIRAL_TYPE_IQ4_NL> : FmtIQ4<SPIRAL_TYPE_IQ4_NL> {};
 template <>
 struct Fmt<SPIRAL_TYPE_IQ4_XS> : FmtIQ4<SPIRAL_TYPE_IQ4_XS> {};
 
+// ---- exact mode ----------------------------------------------------------------
+// Same tasks, payload loads and (for Q4_0, Q6_K and the K-quants) the same x
+// staging as the relaxed forms above; dot() multiplies bf16_rne(code * scale)
+// weights. Q8_0 and IQ4 stage x as plain bf16 (no fp32 widening, no sums).
+
+// x as bf16 in task order, ELEMS per task: entry e of task t holds its
+// elements 8e .. 8e + 7, blocked as lds_task describes.
+template <int ELEMS>
+struct PlainX {
+  static constexpr int kE = ELEMS / 8;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / ELEMS) * kE * 16; }
+  struct X {
+    uint4 xp[kE];
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int /*T*/, int t) {
+    const uint8_t* e = lds + lds_task(t, kE);
+#pragma unroll
+    for (int i = 0; i < kE; ++i) x.xp[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+  }
+  // Item = one 16-byte entry (8 consecutive x): item e is entry e % kE of
+  // task e / kE, which is x[8 e .. 8 e + 7]. Loads past the end reread the
+  // last item (no branch around them) and are not stored.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const uint32_t items = static_cast<uint32_t>(k / 8);
+    const uint4* src = reinterpret_cast<const uint4*>(x);
+    for (uint32_t e0 = threadIdx.x; e0 < items; e0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) v[u] = src[min(e0 + u * blockDim.x, items - 1)];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const uint32_t e = e0 + u * blockDim.x;
+        if (e < items)
+          *reinterpret_cast<uint4*>(lds + lds_task(static_cast<int>(e / kE), kE) + 1024u * (e % kE)) = v[u];
+      }
+    }
+  }
+};
+
+template <int TYPE>
+struct Exact;
+
+// Q4_0: low nibbles c as fp16 1024 + c, (1024 + c) d - 1032 d = (c - 8) d;
+// high nibbles masked in place (byte 16 c) as fp16 64 + c, (64 + c) d - 72 d.
+// Both offset terms are exact in fp32 (129 * 8 d, 9 * 8 d).
+template <>
+struct Exact<SPIRAL_TYPE_Q4_0> : Fmt<SPIRAL_TYPE_Q4_0> {
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const float d = fp16_scale(p.d);
+    const float cl = -1032.0f * d, ch = -72.0f * d;
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = w[i] & 0xF0F0F0F0u;
+      const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
+      s0 = dot2(wpair<kHi1024, kSel01>(lo, d, cl), (i & 1) ? el.z : el.x, s0);
+      s1 = dot2(wpair<kHi1024, kSel23>(lo, d, cl), (i & 1) ? el.w : el.y, s1);
+      s0 = dot2(wpair<kHi64, kSel01>(hi, d, ch), (i & 1) ? eh.z : eh.x, s0);
+      s1 = dot2(wpair<kHi64, kSel23>(hi, d, ch), (i & 1) ? eh.w : eh.y, s1);
+    }
+    return s0 + s1;
+  }
+};
+
+// Q8_0: q + 128 (q ^ 0x80) as fp16 1024 + q + 128, minus 1152 d (9 * 128 d).
+template <>
+struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
+  using XS = PlainX<16>;
+  static constexpr int kE = XS::kE;
+  using X = XS::X;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return XS::lds_bytes(k); }
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) { XS::xload(x, lds, T, t); }
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) { XS::stage(x, k, lds); }
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const float d = fp16_scale(p.d);
+    const float c = -1152.0f * d;
+    const uint32_t w[4] = {p.q.x ^ 0x80808080u, p.q.y ^ 0x80808080u, p.q.z ^ 0x80808080u, p.q.w ^ 0x80808080u};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 e = x.xp[i >> 1];
+      s0 = dot2(wpair<kHi1024, kSel01>(w[i], d, c), (i & 1) ? e.z : e.x, s0);
+      s1 = dot2(wpair<kHi1024, kSel23>(w[i], d, c), (i & 1) ? e.w : e.y, s1);
+    }
+    return s0 + s1;
+  }
+};
+
+// Q6_K: the 6-bit code q of each element is assembled shifted up by two
+// (bits 2..7 of its byte), so the fp16 under 0x64 is 1024 + 4 q; with the
+// group's ds = d * sc, (1024 + 4 q) (ds / 4) - 288 ds = (q - 32) ds. ds / 4
+// and 288 ds (9 * 32 ds, ds at most 19 significant bits) are exact.
+template <>
+struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
+  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
+    const uint32_t A[4] = {p.a.x, p.a.y, p.a.z, p.a.w}, B[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
+    const uint32_t H[4] = {p.h.x, p.h.y, p.h.z, p.h.w};
+    const float d = fp16_scale(p.d);
+    const float dq = 0.25f * d, dc = -288.0f * d;
+    float sq[4], sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float s = static_cast<float>(static_cast<int8_t>((p.sc >> (8 * j)) & 0xffu));
+      sq[j] = dq * s;
+      sc[j] = dc * s;
+    }
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // 4 q of elements 4q .. 4q+3 of each group, one per byte.
+      const uint32_t c[4] = {
+          ((A[q] << 2) & 0x3C3C3C3Cu) | ((H[q] << 6) & 0xC0C0C0C0u),
+          ((B[q] << 2) & 0x3C3C3C3Cu) | ((H[q] << 4) & 0xC0C0C0C0u),
+          ((A[q] >> 2) & 0x3C3C3C3Cu) | ((H[q] << 2) & 0xC0C0C0C0u),
+          ((B[q] >> 2) & 0x3C3C3C3Cu) | (H[q] & 0xC0C0C0C0u),
+      };
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 xv = x.x[2 * j + (q >> 1)];
+        s0 = dot2(wpair<kHi1024, kSel01>(c[j], sq[j], sc[j]), (q & 1) ? xv.z : xv.x, s0);
+        s1 = dot2(wpair<kHi1024, kSel23>(c[j], sq[j], sc[j]), (q & 1) ? xv.w : xv.y, s1);
+      }
+    }
+    return s0 + s1;
+  }
+};
+
+// Q4_K / Q5_K: weight bf16_rne(fma(d * scale, q, -dmin * min)). The code is
+// the subnormal fp16 q * 2^-24, so v_fma_mix_f32 against d * scale * 2^24
+// (exact) and -dmin * min rounds q * d * scale - dmin * min once, as fmaf
+// does; fp16 denormals are kept (the kernels run with fp16 denormals on).
+template <int TYPE>
+struct ExactKQ : FmtKQ<TYPE> {
+  using B = FmtKQ<TYPE>;
+  static __device__ __forceinline__ float dot(const typename B::Payload& p, const typename B::X& x) {
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
+    const uint32_t h[4] = {p.qh.x, p.qh.y, p.qh.z, p.qh.w};
+    const uint32_t sl = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2));
+    const uint32_t sh = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2) + 1);
+    const float d24 = fp16_ieee(p.meta.x & 0xffffu) * kTwo24, dmin = fp16_ieee(p.meta.x >> 16);
+    const float dl = d24 * static_cast<float>(sl & 0xffu), ml = -(dmin * static_cast<float>(sl >> 8));
+    const float dh = d24 * static_cast<float>(sh & 0xffu), mh = -(dmin * static_cast<float>(sh >> 8));
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      if constexpr (B::kQ5) {
+        lo |= ((h[i] >> p.c2) & 0x01010101u) << 4;
+        hi |= ((h[i] >> (p.c2 + 1)) & 0x01010101u) << 4;
+      }
+      const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
+      s0 = dot2(wpair<kHiSub, kSel01>(lo, dl, ml), (i & 1) ? el.z : el.x, s0);
+      s1 = dot2(wpair<kHiSub, kSel23>(lo, dl, ml), (i & 1) ? el.w : el.y, s1);
+      s0 = dot2(wpair<kHiSub, kSel01>(hi, dh, mh), (i & 1) ? eh.z : eh.x, s0);
+      s1 = dot2(wpair<kHiSub, kSel23>(hi, dh, mh), (i & 1) ? eh.w : eh.y, s1);
+    }
+    return s0 + s1;
+  }
+};
+template <>
+struct Exact<SPIRAL_TYPE_Q4_K> : ExactKQ<SPIRAL_TYPE_Q4_K> {};
+template <>
+struct Exact<SPIRAL_TYPE_Q5_K> : ExactKQ<SPIRAL_TYPE_Q5_K> {};
+
+// IQ4_NL / IQ4_XS: codebook bytes kv + 128 as fp16 1024 + kv + 128 against
+// the (sub-)block scale s, minus 1152 s (s at most 17 significant bits).
+template <int TYPE>
+struct ExactIQ4 : FmtIQ4<TYPE> {
+  using B = FmtIQ4<TYPE>;
+  using XS = PlainX<32>;
+  static constexpr int kE = XS::kE;
+  using X = typename XS::X;
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return XS::lds_bytes(k); }
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) { XS::xload(x, lds, T, t); }
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) { XS::stage(x, k, lds); }
+  static __device__ __forceinline__ float dot(const typename B::Payload& p, const X& x) {
+    const float s = B::kXS ? iq4xs_scale(p.m, p.sub) : fp16_ieee(p.m.x);
+    const float c = -1152.0f * s;
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = iq4_lut(w[i] & 0x0F0F0F0Fu), hi = iq4_lut((w[i] >> 4) & 0x0F0F0F0Fu);
+      const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
+      s0 = dot2(wpair<kHi1024, kSel01>(lo, s, c), (i & 1) ? el.z : el.x, s0);
+      s1 = dot2(wpair<kHi1024, kSel23>(lo, s, c), (i & 1) ? el.w : el.y, s1);
+      s0 = dot2(wpair<kHi1024, kSel01>(hi, s, c), (i & 1) ? eh.z : eh.x, s0);
+      s1 = dot2(wpair<kHi1024, kSel23>(hi, s, c), (i & 1) ? eh.w : eh.y, s1);
+    }
+    return s0 + s1;
+  }
+};
+template <>
+struct Exact<SPIRAL_TYPE_IQ4_NL> : ExactIQ4<SPIRAL_TYPE_IQ4_NL> {};
+template <>
+struct Exact<SPIRAL_TYPE_IQ4_XS> : ExactIQ4<SPIRAL_TYPE_IQ4_XS> {};
+
 // ---- the kernel --------------------------------------------------------------
 
-template <int TYPE, int J>
+template <class F, int J>
 struct Unit {
-  typename Fmt<TYPE>::Payload p[J];
+  typename F::Payload p[J];
 };
 
 // Requests the payload of pass `pass` of row `r`; tasks past the row's end
 // load task 0 (a valid address) and are masked out in compute_unit.
-template <int TYPE, int J, bool MASK>
-__device__ __forceinline__ void load_unit(Unit<TYPE, J>& U, const uint8_t* w, int64_t n_rows, int64_t k,
+template <class F, int J, bool MASK>
+__device__ __forceinline__ void load_unit(Unit<F, J>& U, const uint8_t* w, int64_t n_rows, int64_t k,
                                           int64_t r, int pass, int T, int lane) {
-  using F = Fmt<TYPE>;
   const typename F::Row R = F::row(w, n_rows, k, r);
 #pragma unroll
   for (int j = 0; j < J; ++j) {
@@ -625,14 +850,14 @@ __device__ __forceinline__ void store_y(void* y, int64_t r, float v) {
     static_cast<__bf16*>(y)[r] = static_cast<__bf16>(v);
 }
 
+// F: the format's arithmetic (Exact<TYPE> or the relaxed Fmt<TYPE>).
 // XREG: the row fits one pass (T <= 64 J) and each lane keeps the x of its J
 // tasks in registers. MASK: some tasks of a pass fall past the row's end.
 // DEPTH: units whose payload is in flight at once (a ring of DEPTH buffers).
-template <int TYPE, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT>
+template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT>
 __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
                                                           int64_t k, const uint16_t* __restrict__ x,
                                                           void* __restrict__ y) {
-  using F = Fmt<TYPE>;
   extern __shared__ __align__(16) uint8_t lds[];
   const int lane = threadIdx.x & 63;
   const int64_t wave =
@@ -645,7 +870,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restr
 
   // Unit coordinates advance one pass at a time: (rl, pl) for loads, (rc, pc)
   // for compute.
-  Unit<TYPE, J> buf[DEPTH];
+  Unit<F, J> buf[DEPTH];
   int64_t rl = r0;
   int pl = 0;
   auto advance = [&](int64_t& r, int& pass) {
@@ -654,7 +879,7 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restr
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) {
     if (d < units) {
-      load_unit<TYPE, J, MASK>(buf[d], w, n_rows, k, rl, pl, T, lane);
+      load_unit<F, J, MASK>(buf[d], w, n_rows, k, rl, pl, T, lane);
       advance(rl, pl);
     }
   }
@@ -699,98 +924,122 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restr
       }
       advance(rc, pc);
       if (u + DEPTH < units) {
-        load_unit<TYPE, J, MASK>(buf[d], w, n_rows, k, rl, pl, T, lane);
+        load_unit<F, J, MASK>(buf[d], w, n_rows, k, rl, pl, T, lane);
         advance(rl, pl);
       }
     }
   }
 }
 
-template <int TYPE, int J, int WAVES, int DEPTH, bool XREG, bool MASK>
+template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK>
 int launch_cfg(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
-  const int64_t lds = Fmt<TYPE>::lds_bytes(k);
+  const int64_t lds = F::lds_bytes(k);
   const void* kern = y_type == SPIRAL_TYPE_F32
-                         ? reinterpret_cast<const void*>(gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, true>)
-                         : reinterpret_cast<const void*>(gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, false>);
+                         ? reinterpret_cast<const void*>(gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, true>)
+                         : reinterpret_cast<const void*>(gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, false>);
   const int64_t resident = static_cast<int64_t>(device_cu_count()) * blocks_per_cu(kern, 64 * WAVES, lds);
   const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n_rows, WAVES), resident)));
   const uint8_t* W = static_cast<const uint8_t*>(w);
   if (y_type == SPIRAL_TYPE_F32)
-    hipLaunchKernelGGL((gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, true>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
+    hipLaunchKernelGGL((gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, true>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
                        n_rows, k, x, y);
   else
-    hipLaunchKernelGGL((gemv_kernel<TYPE, J, WAVES, DEPTH, XREG, MASK, false>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
+    hipLaunchKernelGGL((gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, false>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
                        n_rows, k, x, y);
   return launch_status();
 }
 
-template <int TYPE, int J, int WAVES, int DEPTH>
+template <class F, int J, int WAVES, int DEPTH>
 int launch_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
-  const int64_t T = k / Fmt<TYPE>::kTaskElems;
+  const int64_t T = k / F::kTaskElems;
   const bool xreg = T <= 64 * J, mask = T % (64 * J) != 0;
   if (xreg)
-    return mask ? launch_cfg<TYPE, J, WAVES, DEPTH, true, true>(w, n_rows, k, x, y, y_type, s)
-                : launch_cfg<TYPE, J, WAVES, DEPTH, true, false>(w, n_rows, k, x, y, y_type, s);
-  return mask ? launch_cfg<TYPE, J, WAVES, DEPTH, false, true>(w, n_rows, k, x, y, y_type, s)
-              : launch_cfg<TYPE, J, WAVES, DEPTH, false, false>(w, n_rows, k, x, y, y_type, s);
+    return mask ? launch_cfg<F, J, WAVES, DEPTH, true, true>(w, n_rows, k, x, y, y_type, s)
+                : launch_cfg<F, J, WAVES, DEPTH, true, false>(w, n_rows, k, x, y, y_type, s);
+  return mask ? launch_cfg<F, J, WAVES, DEPTH, false, true>(w, n_rows, k, x, y, y_type, s)
+              : launch_cfg<F, J, WAVES, DEPTH, false, false>(w, n_rows, k, x, y, y_type, s);
 }
 
-// J = tasks per lane per unit, chosen so that rows of up to 64 J tasks keep x
-// in registers; two units in flight per wave (measured best on MI355X for
-// the 4096x14336 Q6_K, 14336x4096 Q8_0 and 4096x4096 Q4_0 shapes). Q6_K keeps
-// x in LDS (64 bf16 per task) with J = 1, in 16-wave workgroups (x staged
-// once per 16 rows; 5 % faster than 8 waves on the 4096x14336 shape, while
-// deeper rings, two tasks per lane and fewer resident workgroups were slower).
-// Kernels whose registers allow three waves a SIMD but not four (Q8_0 at
-// J = 4, 138 VGPRs; Q5_K at J = 2, 133) run 12-wave workgroups, one a CU,
-// instead of leaving a third of the slots empty: 14336x4096 Q8_0 11.73 us
-// against 11.83 for 8 waves and Q5_K 10.86 against 11.65 (medians), while
-// 4- and 6-wave workgroups and a third ring slot were slower for Q8_0.
-// Those that fit four (Q4_0, Q4_K, IQ4) keep two 8-wave workgroups a CU:
-// 12- and 10-wave ones were 2-20 % slower.
+// Relaxed mode. J = tasks per lane per unit, chosen so that rows of up to
+// 64 J tasks keep x in registers; two units in flight per wave (measured best
+// on MI355X for the 4096x14336 Q6_K, 14336x4096 Q8_0 and 4096x4096 Q4_0
+// shapes). Q6_K keeps x in LDS (64 bf16 per task) with J = 1, in 16-wave
+// workgroups (x staged once per 16 rows; 5 % faster than 8 waves on the
+// 4096x14336 shape, while deeper rings, two tasks per lane and fewer
+// resident workgroups were slower). Kernels whose registers allow three
+// waves a SIMD but not four (Q8_0 at J = 4, 138 VGPRs; Q5_K at J = 2, 133)
+// run 12-wave workgroups, one a CU, instead of leaving a third of the slots
+// empty: 14336x4096 Q8_0 11.73 us against 11.83 for 8 waves and Q5_K 10.86
+// against 11.65 (medians), while 4- and 6-wave workgroups and a third ring
+// slot were slower for Q8_0. Those that fit four (Q4_0, Q4_K, IQ4) keep two
+// 8-wave workgroups a CU: 12- and 10-wave ones were 2-20 % slower, so rows
+// longer than 128 tasks (J = 4) take 12 waves only for Q8_0.
 template <int TYPE>
-int launch_gemv(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
-  const int64_t T = k / Fmt<TYPE>::kTaskElems;
-  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<TYPE, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 64) return launch_j<TYPE, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 128) return launch_j<TYPE, 2, TYPE == SPIRAL_TYPE_Q5_K ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
-  return launch_j<TYPE, 4, 12, 2>(w, n_rows, k, x, y, y_type, s);
+int launch_relaxed(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  using F = Fmt<TYPE>;
+  const int64_t T = k / F::kTaskElems;
+  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 64) return launch_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 128) return launch_j<F, 2, TYPE == SPIRAL_TYPE_Q5_K ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
+  return launch_j<F, 4, TYPE == SPIRAL_TYPE_Q8_0 ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
+}
+
+// Exact mode: the same unit shapes.
+template <int TYPE>
+int launch_exact(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  using F = Exact<TYPE>;
+  const int64_t T = k / F::kTaskElems;
+  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 64) return launch_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 128) return launch_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  return launch_j<F, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
+}
+
+template <int TYPE>
+int launch_gemv(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, bool exact,
+                hipStream_t s) {
+  return exact ? launch_exact<TYPE>(w, n_rows, k, x, y, y_type, s) : launch_relaxed<TYPE>(w, n_rows, k, x, y, y_type, s);
 }
 
 }  // namespace
 
 // Largest k the LDS-staged GEMV accepts (64 KiB of staged x).
-template <int TYPE>
+template <class F>
 int64_t max_k_of() {
-  using F = Fmt<TYPE>;
   const int64_t per_task = F::lds_bytes(64 * F::kTaskElems) / 64;
   return (kMaxLds / per_task / 64) * 64 * F::kTaskElems;
 }
 
-int64_t gemv_max_k(int type) {
+template <int TYPE>
+int64_t max_k_mode(bool exact) {
+  return exact ? max_k_of<Exact<TYPE>>() : max_k_of<Fmt<TYPE>>();
+}
+
+int64_t gemv_max_k(int type, bool exact) {
   switch (type) {
-    case SPIRAL_TYPE_Q4_0: return max_k_of<SPIRAL_TYPE_Q4_0>();
-    case SPIRAL_TYPE_Q8_0: return max_k_of<SPIRAL_TYPE_Q8_0>();
-    case SPIRAL_TYPE_Q6_K: return max_k_of<SPIRAL_TYPE_Q6_K>();
-    case SPIRAL_TYPE_Q4_K: return max_k_of<SPIRAL_TYPE_Q4_K>();
-    case SPIRAL_TYPE_Q5_K: return max_k_of<SPIRAL_TYPE_Q5_K>();
-    case SPIRAL_TYPE_IQ4_NL: return max_k_of<SPIRAL_TYPE_IQ4_NL>();
-    case SPIRAL_TYPE_IQ4_XS: return max_k_of<SPIRAL_TYPE_IQ4_XS>();
+    case SPIRAL_TYPE_Q4_0: return max_k_mode<SPIRAL_TYPE_Q4_0>(exact);
+    case SPIRAL_TYPE_Q8_0: return max_k_mode<SPIRAL_TYPE_Q8_0>(exact);
+    case SPIRAL_TYPE_Q6_K: return max_k_mode<SPIRAL_TYPE_Q6_K>(exact);
+    case SPIRAL_TYPE_Q4_K: return max_k_mode<SPIRAL_TYPE_Q4_K>(exact);
+    case SPIRAL_TYPE_Q5_K: return max_k_mode<SPIRAL_TYPE_Q5_K>(exact);
+    case SPIRAL_TYPE_IQ4_NL: return max_k_mode<SPIRAL_TYPE_IQ4_NL>(exact);
+    case SPIRAL_TYPE_IQ4_XS: return max_k_mode<SPIRAL_TYPE_IQ4_XS>(exact);
     default: return 0;
   }
 }
 
-// y[n] = sum_k W[n][k] x[k]; arguments validated by the caller (k <= gemv_max_k).
-int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type,
+// y[n] = sum_k W[n][k] x[k]; arguments validated by the caller
+// (k <= gemv_max_k(type, exact)).
+int gemv(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, bool exact,
          hipStream_t s) {
   switch (type) {
-    case SPIRAL_TYPE_Q4_0: return launch_gemv<SPIRAL_TYPE_Q4_0>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_Q8_0: return launch_gemv<SPIRAL_TYPE_Q8_0>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_Q6_K: return launch_gemv<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_Q4_K: return launch_gemv<SPIRAL_TYPE_Q4_K>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_Q5_K: return launch_gemv<SPIRAL_TYPE_Q5_K>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_IQ4_NL: return launch_gemv<SPIRAL_TYPE_IQ4_NL>(w, n_rows, k, x, y, y_type, s);
-    case SPIRAL_TYPE_IQ4_XS: return launch_gemv<SPIRAL_TYPE_IQ4_XS>(w, n_rows, k, x, y, y_type, s);
+    case SPIRAL_TYPE_Q4_0: return launch_gemv<SPIRAL_TYPE_Q4_0>(w, n_rows, k, x, y, y_type, exact, s);
+    case SPIRAL_TYPE_Q8_0: return launch_gemv<SPIRAL_TYPE_Q8_0>(w, n_rows, k, x, y, y_type, exact, s);
+    case SPIRAL_TYPE_Q6_K: return launch_gemv<SPIRAL_TYPE_Q6_K>(w, n_rows, k, x, y, y_type, exact, s);
+    case SPIRAL_TYPE_Q4_K: return launch_gemv<SPIRAL_TYPE_Q4_K>(w, n_rows, k, x, y, y_type, exact, s);
+    case SPIRAL_TYPE_Q5_K: return launch_gemv<SPIRAL_TYPE_Q5_K>(w, n_rows, k, x, y, y_type, exact, s);
+    case SPIRAL_TYPE_IQ4_NL: return launch_gemv<SPIRAL_TYPE_IQ4_NL>(w, n_rows, k, x, y, y_type, exact, s);
+    case SPIRAL_TYPE_IQ4_XS: return launch_gemv<SPIRAL_TYPE_IQ4_XS>(w, n_rows, k, x, y, y_type, exact, s);
     default: return SPIRAL_ERR_TYPE;
   }
 }

@@ -95,6 +95,21 @@ def mul_mat(qtype, w, n_rows, k, x, out_dtype=torch.bfloat16, out=None, workspac
     return out
 
 
+def gemv_relaxed(qtype, w, n_rows, k, x, out_dtype=torch.bfloat16, out=None):
+    """The named relaxed single-row product (spiral_gemv_relaxed): the block
+    scale multiplies each block's fp32 sum, so weights are not rounded to
+    bf16 first. x is [k] (or [1, k]) bfloat16; returns [1, n_rows]."""
+    _require_cuda(w, x)
+    x = x.reshape(-1)
+    if x.dtype != torch.bfloat16 or x.numel() != k or not x.is_contiguous():
+        raise ValueError("x must be k contiguous bfloat16 values")
+    if out is None:
+        out = torch.empty((1, n_rows), dtype=out_dtype, device=w.device)
+    check(lib().spiral_gemv_relaxed(qtype, _ptr(w), n_rows, k, _ptr(x), _ptr(out), _out_type(out.dtype),
+                                    _stream()), "gemv_relaxed")
+    return out
+
+
 def mul_mat_id_workspace(n_expert, n_tokens, top_k, device):
     n = lib().spiral_mul_mat_id_workspace_bytes(n_expert, n_tokens, top_k)
     return torch.empty(max(n, 16), dtype=torch.uint8, device=device)

@@ -4,12 +4,15 @@ Bars:
   - layout conversion, dequant, GET_ROWS, reference-record unpack: bit-exact
     (uint16 bf16 patterns compared with array_equal, zero signs included);
   - products: max |y - y_ref| / max(|y_ref|, rms(y_ref)) <= 1e-2 against a
-    float64 oracle over the exact bf16 weights (REL_TOL); the dense and MoE
-    GEMMs use bf16 weights like the reference and are also held to 1e-3 with
-    float32 output (REL_TOL_EXACT_W). The GEMV multiplies by the unrounded
-    weights (the block scale applied to each block's code sum) and is also
-    held to 1e-4 with float32 output against a float64 oracle over those
-    weights (REL_TOL_UNROUNDED_W).
+    float64 oracle over the exact bf16 weights (REL_TOL); every product form
+    (GEMV, small batch, GEMM, MoE) multiplies those bf16 weights like the
+    reference and is also held to 1e-3 with float32 output
+    (REL_TOL_EXACT_W), where only fp32 summation order remains;
+  - the named relaxed GEMV (spiral_gemv_relaxed: the block scale applied to
+    each block's code sum, weights never rounded to bf16) is held to its own
+    bar: 1e-4 with float32 output against a float64 oracle over the
+    unrounded weights (REL_TOL_UNROUNDED_W), and only 2e-2 against the
+    bf16-weight oracle (REL_TOL_RELAXED).
 """
 
 import numpy as np
@@ -24,6 +27,7 @@ pytestmark = pytest.mark.gpu
 REL_TOL = 1e-2
 REL_TOL_EXACT_W = 1e-3
 REL_TOL_UNROUNDED_W = 1e-4
+REL_TOL_RELAXED = 2e-2
 FORMATS = [O.Q4_0, O.Q8_0, O.Q6_K]
 NAMES = {O.Q4_0: "q4_0", O.Q8_0: "q8_0", O.Q6_K: "q6_k"}
 
@@ -151,36 +155,130 @@ def _mul_mat_case(cuda, qtype, n, k, m, seed, out_dtype, unrounded=False):
     return y.float().cpu().numpy(), ref
 
 
+def gemv_bar(out_dtype):
+    return REL_TOL if out_dtype == torch.bfloat16 else REL_TOL_EXACT_W
+
+
 @pytest.mark.parametrize("qtype", FORMATS)
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_gemv_small(cuda, qtype, out_dtype):
     k = O.BLOCK_ELEMS[qtype] * 12
     for n in (1, 7, 129):
-        y, ref, ref_u = _mul_mat_case(cuda, qtype, n, k, 1, 20 + n, out_dtype, unrounded=True)
-        assert rel_err(y, ref) <= REL_TOL, (n, rel_err(y, ref))
-        if out_dtype == torch.float32:
-            assert rel_err(y, ref_u) <= REL_TOL_UNROUNDED_W, (n, rel_err(y, ref_u))
+        y, ref = _mul_mat_case(cuda, qtype, n, k, 1, 20 + n, out_dtype)
+        assert rel_err(y, ref) <= gemv_bar(out_dtype), (n, rel_err(y, ref))
 
 
 @pytest.mark.parametrize("k_blocks", [17, 65, 127, 129, 192, 257])
 def test_gemv_q8_0_scale_spans(cuda, k_blocks):
-    """The Q8_0 GEMV loads a unit's scales one dword per lane and spreads
-    them across lanes: rows with an odd number of blocks start in the upper
-    half of a dword on odd rows (37 rows), one pass in registers (17: one
-    task per lane, 65 and 127: four) or several passes (129 and 257: a
-    128-scale span can cover 65 dwords; 192: even)."""
+    """Rows with an odd number of blocks, one pass with x in registers (17:
+    one task per lane, 65 and 127: four) or several passes from LDS (129 and
+    257, a masked last pass; 192: even)."""
     k = 32 * k_blocks
-    y, ref, ref_u = _mul_mat_case(cuda, O.Q8_0, 37, k, 1, 40 + k_blocks, torch.float32, unrounded=True)
-    assert rel_err(y, ref) <= REL_TOL, rel_err(y, ref)
-    assert rel_err(y, ref_u) <= REL_TOL_UNROUNDED_W, rel_err(y, ref_u)
+    y, ref = _mul_mat_case(cuda, O.Q8_0, 37, k, 1, 40 + k_blocks, torch.float32)
+    assert rel_err(y, ref) <= REL_TOL_EXACT_W, rel_err(y, ref)
 
 
-@pytest.mark.parametrize("qtype,n,k", [(O.Q8_0, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q4_0, 4096, 4096)])
-def test_gemv_workload_shapes(cuda, qtype, n, k):
-    y, ref = _mul_mat_case(cuda, qtype, n, k, 1, 3, torch.bfloat16)
-    err = rel_err(y, ref)
-    print(f"gemv {NAMES[qtype]} {n}x{k}: rel err {err:.2e}")
-    assert err <= REL_TOL
+@pytest.mark.parametrize("qtype,n,k", [(O.Q8_0, 14336, 4096), (O.Q6_K, 4096, 14336), (O.Q4_0, 4096, 4096),
+                                       (O.Q4_0, 4096, 14336)])
+@pytest.mark.parametrize("seed", [3, 11, 29])
+def test_gemv_workload_shapes(cuda, qtype, n, k, seed):
+    """The decode workloads at full size over three seeds, both outputs."""
+    for out_dtype in (torch.float32, torch.bfloat16):
+        y, ref = _mul_mat_case(cuda, qtype, n, k, 1, seed, out_dtype)
+        err = rel_err(y, ref)
+        print(f"gemv {NAMES[qtype]} {n}x{k} seed {seed} {out_dtype}: rel err {err:.2e}")
+        assert err <= gemv_bar(out_dtype)
+
+
+# The reference's first model target instantiates these single-row products
+# (src/quants/TODO.md:48-51): K = 1536 / 2048 / 4096 against
+# N = 256 / 512 / 2048 / 4096 / 6144 / 12288.
+GEMMA_K = (1536, 2048, 4096)
+GEMMA_N = (256, 512, 2048, 4096, 6144, 12288)
+
+
+@pytest.mark.parametrize("k", GEMMA_K)
+def test_gemv_gemma_shapes(cuda, k):
+    for i, n in enumerate(GEMMA_N):
+        for qtype in (O.Q4_0, O.Q8_0):
+            y, ref = _mul_mat_case(cuda, qtype, n, k, 1, 300 + i, torch.float32)
+            assert rel_err(y, ref) <= REL_TOL_EXACT_W, (NAMES[qtype], n, k, rel_err(y, ref))
+
+
+@pytest.mark.parametrize("seed", [5, 17])
+def test_gemv_q6_k_output_head(cuda, seed):
+    """The Q6_K tied output head of the same target: K = 1536, N = 262,144
+    (src/quants/TODO.md:49-50), 330 MB of weights. The oracle runs on row
+    ranges of 16,384 rows; both outputs are checked against it."""
+    qtype, n, k = O.Q6_K, 262144, 1536
+    raw = synth.make_weights(qtype, n, k, seed)
+    x = synth.make_x(1, k, seed + 100)
+    w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+    xd = dev_bf16(x, cuda)
+    y32 = ops.mul_mat(qtype, w, n, k, xd, out_dtype=torch.float32).cpu().numpy()[0]
+    y16 = ops.mul_mat(qtype, w, n, k, xd, out_dtype=torch.bfloat16).float().cpu().numpy()[0]
+    del w
+    rb = O.BLOCK_BYTES[qtype] * (k // O.BLOCK_ELEMS[qtype])
+    ref = np.empty(n, dtype=np.float64)
+    step = 16384
+    for r0 in range(0, n, step):
+        chunk = raw[r0 * rb:(r0 + step) * rb]
+        ref[r0:r0 + step] = O.matmul_f64(O.dequant(qtype, chunk, step, k), x)[0]
+    e32, e16 = rel_err(y32, ref), rel_err(y16, ref)
+    print(f"gemv q6_k output head {n}x{k} seed {seed}: f32 {e32:.2e} bf16 {e16:.2e}")
+    assert e32 <= REL_TOL_EXACT_W
+    assert e16 <= REL_TOL
+
+
+def test_gemv_row_is_independent_of_the_batch(cuda):
+    """A row decoded alone (the GEMV) and inside a batch (the small-batch
+    form at m = 4) multiplies the same bf16 weights: the outputs agree to
+    fp32 summation order."""
+    for qtype in FORMATS:
+        n, k = 300, O.BLOCK_ELEMS[qtype] * 24
+        raw = synth.make_weights(qtype, n, k, 77)
+        x = synth.make_x(4, k, 78)
+        w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+        xd = dev_bf16(x, cuda)
+        batch = ops.mul_mat(qtype, w, n, k, xd, out_dtype=torch.float32).cpu().numpy()
+        for i in range(4):
+            one = ops.mul_mat(qtype, w, n, k, xd[i:i + 1], out_dtype=torch.float32).cpu().numpy()[0]
+            assert rel_err(one, batch[i]) <= 1e-5, (NAMES[qtype], i, rel_err(one, batch[i]))
+
+
+# ---- the named relaxed GEMV ----------------------------------------------------
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_gemv_relaxed(cuda, qtype):
+    """spiral_gemv_relaxed against its own oracle (unrounded weights) to 1e-4
+    and the bf16-weight oracle only to 2e-2, one pass in registers and
+    several from LDS."""
+    for n, kb in ((7, 12), (129, 160 if qtype != O.Q6_K else 24)):
+        k = O.BLOCK_ELEMS[qtype] * kb
+        raw = synth.make_weights(qtype, n, k, 50 + n)
+        x = synth.make_x(1, k, 51 + n)
+        w = ops.to_planar(qtype, dev_u8(raw, cuda), n, k)
+        y = ops.gemv_relaxed(qtype, w, n, k, dev_bf16(x, cuda), out_dtype=torch.float32).cpu().numpy()
+        ref_u = O.matmul_f64_exact(O.dequant_exact(qtype, raw, n, k), x)
+        ref = O.matmul_f64(O.dequant(qtype, raw, n, k), x)
+        assert rel_err(y, ref_u) <= REL_TOL_UNROUNDED_W, rel_err(y, ref_u)
+        assert rel_err(y, ref) <= REL_TOL_RELAXED, rel_err(y, ref)
+
+
+def test_gemv_relaxed_limits(cuda):
+    from spiral_amd._lib import lib
+    L = lib()
+    for qtype in FORMATS:
+        assert L.spiral_gemv_relaxed_max_k(qtype) >= 14336
+    assert L.spiral_gemv_relaxed_max_k(0) == 0
+    qtype, n = O.Q4_0, 8
+    k = (L.spiral_gemv_relaxed_max_k(qtype) // 32 + 1) * 32
+    w = torch.zeros(n * k // 32 * 18, dtype=torch.uint8, device=cuda)
+    x = torch.zeros(k, dtype=torch.bfloat16, device=cuda)
+    y = torch.zeros(n, dtype=torch.float32, device=cuda)
+    from spiral_amd.ops import _ptr, _stream
+    assert L.spiral_gemv_relaxed(qtype, _ptr(w), n, k, _ptr(x), _ptr(y), 0, _stream()) == 1  # SPIRAL_ERR_SHAPE
+    assert L.spiral_gemv_relaxed(qtype, _ptr(w), n, 48, _ptr(x), _ptr(y), 0, _stream()) == 1
 
 
 def test_gemv_catches_a_planted_oracle_error(cuda):

@@ -34,8 +34,8 @@ pytestmark = pytest.mark.gpu
 
 FORMATS = [O.Q4_0, O.Q8_0, O.Q6_K]
 TOL_BF16_OUT = 1e-2     # bf16 outputs (one rounding of the result)
-TOL_F32_OUT = 1e-3      # float32 outputs of the exact-weight MFMA paths
-TOL_F32_GEMV = 5e-3     # float32 GEMV output: codes unrounded, scale after the block sum
+TOL_F32_OUT = 1e-3      # float32 outputs (every product form multiplies the exact bf16 weights)
+TOL_F32_RELAXED = 5e-3  # the named relaxed GEMV: codes unrounded, scale after the block sum
 
 # fp16 scale patterns with exponent 0 (decode to +0) and exponent 31 / the
 # normal extremes (decode to finite values).
@@ -126,8 +126,20 @@ GEMV_K = {O.Q4_0: (32 * 12, 32 * 288), O.Q8_0: (32 * 12, 32 * 160), O.Q6_K: (256
 def test_gemv_special_weights(cuda, qtype, out_dtype):
     for k in GEMV_K[qtype]:
         y, wb, x = run_mul_mat(cuda, qtype, 67, k, 1, 100 + k, out_dtype)
-        tol = TOL_BF16_OUT if out_dtype == torch.bfloat16 else TOL_F32_GEMV
+        tol = TOL_BF16_OUT if out_dtype == torch.bfloat16 else TOL_F32_OUT
         check_product(y, wb, x, tol)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_gemv_relaxed_special_weights(cuda, qtype):
+    """The named relaxed GEMV decodes the same special scales (exponent 0 to
+    +0, exponent 31 finite) on its own path."""
+    for k in GEMV_K[qtype]:
+        raw = special_weights(qtype, 67, k, 300 + k)
+        x = synth.make_x(1, k, 301 + k)
+        w = ops.to_planar(qtype, dev_u8(raw, cuda), 67, k)
+        y = ops.gemv_relaxed(qtype, w, 67, k, dev_bf16(x, cuda), out_dtype=torch.float32).cpu().numpy()
+        check_product(y, O.dequant(qtype, raw, 67, k), x, TOL_F32_RELAXED)
 
 
 @pytest.mark.parametrize("qtype", FORMATS)

@@ -412,3 +412,36 @@ def test_cpu_baseline_matches_the_oracle(oracle):
     ref = O.matmul_f64(O.dequant(O.Q4_0, q4, n, k), xm)
     got = O.cb_gemm_q4_0(q4, n, k, xm, 4)
     assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+    k6 = 768
+    q6 = synth.make_weights(O.Q6_K, n, k6, 35)
+    assert np.array_equal(O.cb_dequant_q6_k(q6, n, k6, 4), O.dequant(O.Q6_K, q6, n, k6))
+    x6 = synth.make_x(1, k6, 36)
+    ref = O.matmul_f64(O.dequant(O.Q6_K, q6, n, k6), x6)[0]
+    got = O.cb_gemv_q6_k(q6, n, k6, x6, 4)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+def test_cpu_baseline_moe_matches_the_oracle(oracle):
+    """The grouped CPU MoE leg: each (token, slot) equals the oracle's product
+    with its expert, per-slot and shared inputs, an id routed nowhere gives a
+    zero row."""
+    from spiral_amd import synth
+    n_expert, n, k, n_tokens, top_k = 5, 37, 256, 6, 3
+    per = n * k // 32 * 18
+    raws = [synth.make_weights(O.Q4_0, n, k, 60 + e) for e in range(n_expert)]
+    stack = np.concatenate(raws)
+    rng = np.random.default_rng(61)
+    ids = rng.integers(0, n_expert, (n_tokens, top_k)).astype(np.int32)
+    ids[2, 1] = -1
+    ids[4, 0] = n_expert
+    for x_slots in (1, top_k):
+        x = synth.make_x(n_tokens * x_slots, k, 62).reshape(n_tokens, x_slots, k)
+        got = O.cb_moe_q4_0(stack, per, n_expert, n, k, x, ids, 3)
+        for t in range(n_tokens):
+            for s in range(top_k):
+                e = ids[t, s]
+                if not 0 <= e < n_expert:
+                    assert not got[t, s].any()
+                    continue
+                ref = O.matmul_f64(O.dequant(O.Q4_0, raws[e], n, k), x[t, s % x_slots][None])[0]
+                assert np.max(np.abs(got[t, s] - ref)) <= 1e-5 * np.max(np.abs(ref))
