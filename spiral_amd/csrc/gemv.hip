@@ -112,6 +112,39 @@ constexpr uint32_t kSel01 = 0x04010400u, kSel23 = 0x04030402u;
 constexpr uint32_t kHi1024 = 0x64646464u, kHi64 = 0x54545454u, kHiSub = 0u;
 constexpr float kTwo24 = 16777216.0f;
 
+// ---- buffer access for the exact kernel --------------------------------------
+// Raw buffer resources over one wave's rows of a plane. An access whose
+// offset has bit 31 set lies past the buffer (a wave's span is far below
+// 2 GiB): loads return zeros and stores are dropped without touching
+// memory, so the loop issues every access unconditionally and the compiler
+// can wait for exactly the oldest ring slot.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+constexpr uint32_t kSkip = 0x80000000u;
+constexpr int kStreamAux = 2;  // nt: payload read once
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  // Third dword 0x00020000: raw (untyped) 32-bit accesses on gfx9-class GPUs.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+// Accesses take a per-lane offset v (constant across a wave's steps, plus
+// bit 31 for a lane with nothing to read) and a wave-uniform offset s (the
+// row and pass, in a scalar register). A unit past a wave's last reads
+// through a buffer of no records (every access out of range).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_or_none(__amdgpu_buffer_rsrc_t r, bool none) {
+  return none ? __builtin_amdgcn_make_buffer_rsrc(nullptr, 0, 0, 0x00020000) : r;
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  const auto x = __builtin_amdgcn_raw_buffer_load_b128(r, v, s, kStreamAux);
+  return make_uint4(x[0], x[1], x[2], x[3]);
+}
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0);
+  return make_uint2(x[0], x[1]);
+}
+__device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0);
+}
+
 // Blocked LDS layout (see the header): byte offset of entry 0 of task t when
 // a task has E 16-byte entries; entry e adds e KiB.
 __host__ __device__ __forceinline__ uint32_t lds_task(int t, int E) {
@@ -134,6 +167,7 @@ constexpr int kStageUnroll = 4;
 // (128 + c) with v_perm they line up with consecutive x pairs.
 template <>
 struct Fmt<SPIRAL_TYPE_Q4_0> {
+  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 32, kE = 4;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 4); }
 
@@ -216,6 +250,7 @@ struct Fmt<SPIRAL_TYPE_Q4_0> {
 // x entries per task (half block): 4 x float4 = its 16 x. Sum: float.
 template <>
 struct Fmt<SPIRAL_TYPE_Q8_0> {
+  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 16, kE = 4;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 16) * (kE * 16 + 4); }
 
@@ -295,6 +330,7 @@ struct Fmt<SPIRAL_TYPE_Q8_0> {
 // group j at i / 8 * 8 .. + 7, in order. Sum: float4, one per group.
 template <>
 struct Fmt<SPIRAL_TYPE_Q6_K> {
+  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 64, kE = 8;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 64) * (kE * 16 + 16); }
 
@@ -418,6 +454,7 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
 //   sum_i x_i (d sc q_i - dmin m) = d sc (sum x (128 + q) - 128 sum x) - dmin m sum x
 template <int TYPE>
 struct FmtKQ {
+  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 32, kE = 4;
   static constexpr bool kQ5 = TYPE == SPIRAL_TYPE_Q5_K;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 8); }
@@ -531,6 +568,7 @@ struct Fmt<SPIRAL_TYPE_Q5_K> : FmtKQ<SPIRAL_TYPE_Q5_K> {};
 // qs dwords 0..3, entries 4..7 the high-nibble ones). Sum: float.
 template <int TYPE>
 struct FmtIQ4 {
+  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 32, kE = 8;
   static constexpr bool kXS = TYPE == SPIRAL_TYPE_IQ4_XS;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 4); }
@@ -666,89 +704,214 @@ struct PlainX {
 template <int TYPE>
 struct Exact;
 
+// Interface of an exact format F (the kernel's exact branch):
+//   S                 the per-task scale terms its dot product needs;
+//   scale(p, special) S from the hardware fp16 conversion; sets special when
+//                     a scale is one of the reference's special cases;
+//   scale_rule(p)     S from the reference's bit-level scale rule (kRule
+//                     formats, for a unit in which any lane set special);
+//   dot(p, x, s, a0, a1) adds the task's weights times x into a0 / a1.
+// A task whose terms are all zero contributes +0 (each weight is
+// h * 0 + 0), which is how tasks past a row's end are masked.
+
+// Hardware fp16 -> fp32 (v_cvt_f32_f16), which equals the reference's rule
+// (fp16_scale) on exponents 1..30 and on +-0 (-0 gives weights of +0 in
+// every form below); `special` records an exponent-0 non-zero (subnormal:
+// the rule gives +0) or exponent-31 (the rule gives 2^16 (1.m)) pattern.
+__device__ __forceinline__ float fp16_hw(_Float16 hf, bool& special) {
+  // v_cmp_class mask: signaling and quiet NaN, -inf, -subnormal, +subnormal, +inf
+  constexpr int kSpecial = 0x001 | 0x002 | 0x004 | 0x010 | 0x080 | 0x200;
+  special |= __builtin_amdgcn_classh(hf, kSpecial);
+  return static_cast<float>(hf);
+}
+__device__ __forceinline__ uint32_t fp16_bits(_Float16 hf) { return __builtin_bit_cast(uint16_t, hf); }
+// The scale as loaded (a 16-bit buffer load), kept as a half so that the
+// common path converts it directly and only the rule path takes its bits.
+__device__ __forceinline__ _Float16 bload_h(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0)));
+}
+
 // Q4_0: low nibbles c as fp16 1024 + c, (1024 + c) d - 1032 d = (c - 8) d;
 // high nibbles masked in place (byte 16 c) as fp16 64 + c, (64 + c) d - 72 d.
 // Both offset terms are exact in fp32 (129 * 8 d, 9 * 8 d).
 template <>
 struct Exact<SPIRAL_TYPE_Q4_0> : Fmt<SPIRAL_TYPE_Q4_0> {
-  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
-    const float d = fp16_scale(p.d);
-    const float cl = -1032.0f * d, ch = -72.0f * d;
+  static constexpr bool kExact = true, kRule = true;
+  struct Planes {
+    __amdgpu_buffer_rsrc_t qs, d;
+    uint32_t nb;
+  };
+  // rows [r0, r1) of the planes qs[n][nb][16] | d[n][nb]
+  static __device__ __forceinline__ Planes planes(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r0,
+                                                  int64_t r1) {
+    const int64_t nb = k / 32;
+    return Planes{rsrc(w + r0 * nb * 16, (r1 - r0) * nb * 16), rsrc(w + n_rows * nb * 16 + r0 * nb * 2, (r1 - r0) * nb * 2),
+                  static_cast<uint32_t>(nb)};
+  }
+  struct Payload {
+    uint4 q;
+    _Float16 d;
+  };
+  static __device__ __forceinline__ void bload(Payload& p, const Planes& P, bool none, uint32_t rr, uint32_t tb,
+                                               uint32_t lane, uint32_t lsk) {
+    const uint32_t b = rr * P.nb + tb;
+    p.q = bload16(rsrc_or_none(P.qs, none), (lane * 16u) | lsk, b * 16u);
+    p.d = bload_h(rsrc_or_none(P.d, none), (lane * 2u) | lsk, b * 2u);
+  }
+  struct S {
+    float d, cl, ch;
+  };
+  static __device__ __forceinline__ S terms(float d) { return S{d, -1032.0f * d, -72.0f * d}; }
+  static __device__ __forceinline__ S scale(const Payload& p, bool& special) { return terms(fp16_hw(p.d, special)); }
+  static __device__ __forceinline__ S scale_rule(const Payload& p) { return terms(fp16_scale(fp16_bits(p.d))); }
+  static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
     const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
-    float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = w[i] & 0xF0F0F0F0u;
       const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
-      s0 = dot2(wpair<kHi1024, kSel01>(lo, d, cl), (i & 1) ? el.z : el.x, s0);
-      s1 = dot2(wpair<kHi1024, kSel23>(lo, d, cl), (i & 1) ? el.w : el.y, s1);
-      s0 = dot2(wpair<kHi64, kSel01>(hi, d, ch), (i & 1) ? eh.z : eh.x, s0);
-      s1 = dot2(wpair<kHi64, kSel23>(hi, d, ch), (i & 1) ? eh.w : eh.y, s1);
+      a0 = dot2(wpair<kHi1024, kSel01>(lo, s.d, s.cl), (i & 1) ? el.z : el.x, a0);
+      a1 = dot2(wpair<kHi1024, kSel23>(lo, s.d, s.cl), (i & 1) ? el.w : el.y, a1);
+      a0 = dot2(wpair<kHi64, kSel01>(hi, s.d, s.ch), (i & 1) ? eh.z : eh.x, a0);
+      a1 = dot2(wpair<kHi64, kSel23>(hi, s.d, s.ch), (i & 1) ? eh.w : eh.y, a1);
     }
-    return s0 + s1;
   }
 };
 
 // Q8_0: q + 128 (q ^ 0x80) as fp16 1024 + q + 128, minus 1152 d (9 * 128 d).
 template <>
 struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
+  static constexpr bool kExact = true, kRule = true;
+  struct Planes {
+    __amdgpu_buffer_rsrc_t qs, d;
+    uint32_t nb;
+  };
+  // rows [r0, r1) of the planes qs[n][nb][32] | d[n][nb]; task t = half block
+  static __device__ __forceinline__ Planes planes(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r0,
+                                                  int64_t r1) {
+    const int64_t nb = k / 32;
+    return Planes{rsrc(w + r0 * nb * 32, (r1 - r0) * nb * 32), rsrc(w + n_rows * nb * 32 + r0 * nb * 2, (r1 - r0) * nb * 2),
+                  static_cast<uint32_t>(nb)};
+  }
+  struct Payload {
+    uint4 q;
+    _Float16 d;
+  };
+  static __device__ __forceinline__ void bload(Payload& p, const Planes& P, bool none, uint32_t rr, uint32_t tb,
+                                               uint32_t lane, uint32_t lsk) {
+    p.q = bload16(rsrc_or_none(P.qs, none), (lane * 16u) | lsk, rr * P.nb * 32u + tb * 16u);
+    p.d = bload_h(rsrc_or_none(P.d, none), ((lane >> 1) * 2u) | lsk, (rr * P.nb + (tb >> 1)) * 2u);
+  }
   using XS = PlainX<16>;
   static constexpr int kE = XS::kE;
   using X = XS::X;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return XS::lds_bytes(k); }
   static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) { XS::xload(x, lds, T, t); }
   static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) { XS::stage(x, k, lds); }
-  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
-    const float d = fp16_scale(p.d);
-    const float c = -1152.0f * d;
+  struct S {
+    float d, c;
+  };
+  static __device__ __forceinline__ S scale(const Payload& p, bool& special) {
+    const float d = fp16_hw(p.d, special);
+    return S{d, -1152.0f * d};
+  }
+  static __device__ __forceinline__ S scale_rule(const Payload& p) {
+    const float d = fp16_scale(fp16_bits(p.d));
+    return S{d, -1152.0f * d};
+  }
+  static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
     const uint32_t w[4] = {p.q.x ^ 0x80808080u, p.q.y ^ 0x80808080u, p.q.z ^ 0x80808080u, p.q.w ^ 0x80808080u};
-    float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint4 e = x.xp[i >> 1];
-      s0 = dot2(wpair<kHi1024, kSel01>(w[i], d, c), (i & 1) ? e.z : e.x, s0);
-      s1 = dot2(wpair<kHi1024, kSel23>(w[i], d, c), (i & 1) ? e.w : e.y, s1);
+      a0 = dot2(wpair<kHi1024, kSel01>(w[i], s.d, s.c), (i & 1) ? e.z : e.x, a0);
+      a1 = dot2(wpair<kHi1024, kSel23>(w[i], s.d, s.c), (i & 1) ? e.w : e.y, a1);
     }
-    return s0 + s1;
   }
 };
 
-// Q6_K: the 6-bit code q of each element is assembled shifted up by two
-// (bits 2..7 of its byte), so the fp16 under 0x64 is 1024 + 4 q; with the
-// group's ds = d * sc, (1024 + 4 q) (ds / 4) - 288 ds = (q - 32) ds. ds / 4
-// and 288 ds (9 * 32 ds, ds at most 19 significant bits) are exact.
+// Q6_K: the 6-bit code q of each element as fp16 1024 + q; with the group's
+// ds = d * sc, (1024 + q) ds - 1056 ds = (q - 32) ds. ds has at most 18
+// significant bits (an 11-bit significand times |sc| <= 127, or 128 = 2^7),
+// so 1056 ds = 33 * 32 ds has at most 24 and is exact.
 template <>
 struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
-  static __device__ __forceinline__ float dot(const Payload& p, const X& x) {
-    const uint32_t A[4] = {p.a.x, p.a.y, p.a.z, p.a.w}, B[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
-    const uint32_t H[4] = {p.h.x, p.h.y, p.h.z, p.h.w};
-    const float d = fp16_scale(p.d);
-    const float dq = 0.25f * d, dc = -288.0f * d;
-    float sq[4], sc[4];
+  static constexpr bool kExact = true, kRule = true;
+  struct Planes {
+    __amdgpu_buffer_rsrc_t ql, qh, sc, d;
+    uint32_t nb;
+  };
+  // rows [r0, r1) of the planes ql[n][nb][128] | qh[..][64] | sc[..][16] | d[n][nb]
+  static __device__ __forceinline__ Planes planes(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r0,
+                                                  int64_t r1) {
+    const int64_t nb = k / 256, tot = n_rows * nb, n = r1 - r0;
+    return Planes{rsrc(w + r0 * nb * 128, n * nb * 128), rsrc(w + tot * 128 + r0 * nb * 64, n * nb * 64),
+                  rsrc(w + tot * 192 + r0 * nb * 16, n * nb * 16), rsrc(w + tot * 208 + r0 * nb * 2, n * nb * 2),
+                  static_cast<uint32_t>(nb)};
+  }
+  struct Payload {
+    uint4 a, b, h;
+    uint2 sc8;      // the 8 sub-scales of the task's half super-block
+    uint32_t odd;   // 16-lane half: its groups' sub-scales are the odd bytes
+    _Float16 d;
+  };
+  // Task u: super-block u / 4, half (u >> 1) & 1, 16-lane half u & 1 (as
+  // load()). Loaded values are only stored here: arithmetic on them would
+  // make the compiler wait for the load at once.
+  static __device__ __forceinline__ void bload(Payload& p, const Planes& P, bool none, uint32_t rr, uint32_t tb,
+                                               uint32_t lane, uint32_t lsk) {
+    const uint32_t sb = rr * P.nb + (tb >> 2), ls = lane >> 2, hh = (lane >> 1) & 1u, s = lane & 1u;
+    const uint32_t lo = ls * 128u + 64u * hh + 16u * s;
+    const __amdgpu_buffer_rsrc_t ql = rsrc_or_none(P.ql, none);
+    p.a = bload16(ql, lo | lsk, sb * 128u);
+    p.b = bload16(ql, (lo + 32u) | lsk, sb * 128u);
+    p.h = bload16(rsrc_or_none(P.qh, none), (ls * 64u + 32u * hh + 16u * s) | lsk, sb * 64u);
+    p.sc8 = bload8(rsrc_or_none(P.sc, none), (ls * 16u + 8u * hh) | lsk, sb * 16u);
+    p.odd = s;
+    p.d = bload_h(rsrc_or_none(P.d, none), (ls * 2u) | lsk, sb * 2u);
+  }
+  // Sub-scale of group j is sc[8 h + s + 2 j]: bytes s, s + 2, s + 4, s + 6
+  // of the half's 8 sub-scales.
+  static __device__ __forceinline__ uint32_t sub_scales(const Payload& p) {
+    return __builtin_amdgcn_perm(p.sc8.y, p.sc8.x, p.odd ? 0x07050301u : 0x06040200u);
+  }
+  struct S {
+    float ds[4], c[4];
+  };
+  static __device__ __forceinline__ S terms(float d, uint32_t sc4) {
+    S s;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float s = static_cast<float>(static_cast<int8_t>((p.sc >> (8 * j)) & 0xffu));
-      sq[j] = dq * s;
-      sc[j] = dc * s;
+      s.ds[j] = d * static_cast<float>(static_cast<int8_t>((sc4 >> (8 * j)) & 0xffu));
+      s.c[j] = -1056.0f * s.ds[j];
     }
-    float s0 = 0.0f, s1 = 0.0f;
+    return s;
+  }
+  static __device__ __forceinline__ S scale(const Payload& p, bool& special) {
+    return terms(fp16_hw(p.d, special), sub_scales(p));
+  }
+  static __device__ __forceinline__ S scale_rule(const Payload& p) {
+    return terms(fp16_scale(fp16_bits(p.d)), sub_scales(p));
+  }
+  static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
+    const uint32_t A[4] = {p.a.x, p.a.y, p.a.z, p.a.w}, B[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
+    const uint32_t H[4] = {p.h.x, p.h.y, p.h.z, p.h.w};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      // 4 q of elements 4q .. 4q+3 of each group, one per byte.
+      // 6-bit codes of elements 4q .. 4q+3 of each group, one per byte.
       const uint32_t c[4] = {
-          ((A[q] << 2) & 0x3C3C3C3Cu) | ((H[q] << 6) & 0xC0C0C0C0u),
-          ((B[q] << 2) & 0x3C3C3C3Cu) | ((H[q] << 4) & 0xC0C0C0C0u),
-          ((A[q] >> 2) & 0x3C3C3C3Cu) | ((H[q] << 2) & 0xC0C0C0C0u),
-          ((B[q] >> 2) & 0x3C3C3C3Cu) | (H[q] & 0xC0C0C0C0u),
+          (A[q] & 0x0F0F0F0Fu) | ((H[q] << 4) & 0x30303030u),
+          (B[q] & 0x0F0F0F0Fu) | ((H[q] << 2) & 0x30303030u),
+          ((A[q] >> 4) & 0x0F0F0F0Fu) | (H[q] & 0x30303030u),
+          ((B[q] >> 4) & 0x0F0F0F0Fu) | ((H[q] >> 2) & 0x30303030u),
       };
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint4 xv = x.x[2 * j + (q >> 1)];
-        s0 = dot2(wpair<kHi1024, kSel01>(c[j], sq[j], sc[j]), (q & 1) ? xv.z : xv.x, s0);
-        s1 = dot2(wpair<kHi1024, kSel23>(c[j], sq[j], sc[j]), (q & 1) ? xv.w : xv.y, s1);
+        a0 = dot2(wpair<kHi1024, kSel01>(c[j], s.ds[j], s.c[j]), (q & 1) ? xv.z : xv.x, a0);
+        a1 = dot2(wpair<kHi1024, kSel23>(c[j], s.ds[j], s.c[j]), (q & 1) ? xv.w : xv.y, a1);
       }
     }
-    return s0 + s1;
   }
 };
 
@@ -756,18 +919,51 @@ struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
 // the subnormal fp16 q * 2^-24, so v_fma_mix_f32 against d * scale * 2^24
 // (exact) and -dmin * min rounds q * d * scale - dmin * min once, as fmaf
 // does; fp16 denormals are kept (the kernels run with fp16 denormals on).
+// d and dmin are IEEE binary16 (no special cases).
 template <int TYPE>
 struct ExactKQ : FmtKQ<TYPE> {
   using B = FmtKQ<TYPE>;
-  static __device__ __forceinline__ float dot(const typename B::Payload& p, const typename B::X& x) {
-    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
-    const uint32_t h[4] = {p.qh.x, p.qh.y, p.qh.z, p.qh.w};
+  using Payload = typename B::Payload;
+  using X = typename B::X;
+  static constexpr bool kExact = true, kRule = false;
+  struct Planes {
+    __amdgpu_buffer_rsrc_t qs, qh, meta;
+    uint32_t nb;
+  };
+  // rows [r0, r1) of the planes qs[n][nb][128] | (Q5_K) qh[..][32] | meta[..][16]
+  static __device__ __forceinline__ Planes planes(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r0,
+                                                  int64_t r1) {
+    const int64_t nb = k / 256, tot = n_rows * nb, n = r1 - r0;
+    const __amdgpu_buffer_rsrc_t qs = rsrc(w + r0 * nb * 128, n * nb * 128);
+    return Planes{qs, B::kQ5 ? rsrc(w + tot * 128 + r0 * nb * 32, n * nb * 32) : qs,
+                  rsrc(w + tot * (B::kQ5 ? 160 : 128) + r0 * nb * 16, n * nb * 16), static_cast<uint32_t>(nb)};
+  }
+  static __device__ __forceinline__ void bload(Payload& p, const Planes& P, bool none, uint32_t rr, uint32_t tb,
+                                               uint32_t lane, uint32_t lsk) {
+    const uint32_t sb = rr * P.nb + (tb >> 3);
+    p.q = bload16(rsrc_or_none(P.qs, none), (lane * 16u) | lsk, (rr * P.nb * 8u + tb) * 16u);
+    p.meta = bload16(rsrc_or_none(P.meta, none), ((lane >> 3) * 16u) | lsk, sb * 16u);
+    if constexpr (B::kQ5)
+      p.qh = bload16(rsrc_or_none(P.qh, none), ((lane >> 3) * 32u + (lane & 1u) * 16u) | lsk, sb * 32u);
+    p.c2 = lane & 6u;
+  }
+  struct S {
+    float dl, ml, dh, mh;
+  };
+  static __device__ __forceinline__ S scale(const Payload& p, bool&) {
     const uint32_t sl = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2));
     const uint32_t sh = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2) + 1);
     const float d24 = fp16_ieee(p.meta.x & 0xffffu) * kTwo24, dmin = fp16_ieee(p.meta.x >> 16);
-    const float dl = d24 * static_cast<float>(sl & 0xffu), ml = -(dmin * static_cast<float>(sl >> 8));
-    const float dh = d24 * static_cast<float>(sh & 0xffu), mh = -(dmin * static_cast<float>(sh >> 8));
-    float s0 = 0.0f, s1 = 0.0f;
+    return S{d24 * static_cast<float>(sl & 0xffu), -(dmin * static_cast<float>(sl >> 8)),
+             d24 * static_cast<float>(sh & 0xffu), -(dmin * static_cast<float>(sh >> 8))};
+  }
+  static __device__ __forceinline__ S scale_rule(const Payload& p) {
+    bool unused = false;
+    return scale(p, unused);
+  }
+  static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
+    const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
+    const uint32_t h[4] = {p.qh.x, p.qh.y, p.qh.z, p.qh.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
@@ -776,12 +972,11 @@ struct ExactKQ : FmtKQ<TYPE> {
         hi |= ((h[i] >> (p.c2 + 1)) & 0x01010101u) << 4;
       }
       const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
-      s0 = dot2(wpair<kHiSub, kSel01>(lo, dl, ml), (i & 1) ? el.z : el.x, s0);
-      s1 = dot2(wpair<kHiSub, kSel23>(lo, dl, ml), (i & 1) ? el.w : el.y, s1);
-      s0 = dot2(wpair<kHiSub, kSel01>(hi, dh, mh), (i & 1) ? eh.z : eh.x, s0);
-      s1 = dot2(wpair<kHiSub, kSel23>(hi, dh, mh), (i & 1) ? eh.w : eh.y, s1);
+      a0 = dot2(wpair<kHiSub, kSel01>(lo, s.dl, s.ml), (i & 1) ? el.z : el.x, a0);
+      a1 = dot2(wpair<kHiSub, kSel23>(lo, s.dl, s.ml), (i & 1) ? el.w : el.y, a1);
+      a0 = dot2(wpair<kHiSub, kSel01>(hi, s.dh, s.mh), (i & 1) ? eh.z : eh.x, a0);
+      a1 = dot2(wpair<kHiSub, kSel23>(hi, s.dh, s.mh), (i & 1) ? eh.w : eh.y, a1);
     }
-    return s0 + s1;
   }
 };
 template <>
@@ -791,30 +986,71 @@ struct Exact<SPIRAL_TYPE_Q5_K> : ExactKQ<SPIRAL_TYPE_Q5_K> {};
 
 // IQ4_NL / IQ4_XS: codebook bytes kv + 128 as fp16 1024 + kv + 128 against
 // the (sub-)block scale s, minus 1152 s (s at most 17 significant bits).
+// d is IEEE binary16 (no special cases).
 template <int TYPE>
 struct ExactIQ4 : FmtIQ4<TYPE> {
   using B = FmtIQ4<TYPE>;
+  using Payload = typename B::Payload;
+  static constexpr bool kExact = true, kRule = false;
+  struct Planes {
+    __amdgpu_buffer_rsrc_t qs, d;
+    uint32_t nb;
+  };
+  // rows [r0, r1): IQ4_NL qs[n][nb][16] | d[n][nb]; IQ4_XS qs[n][nb][128] | meta[n][nb][8]
+  static __device__ __forceinline__ Planes planes(const uint8_t* w, int64_t n_rows, int64_t k, int64_t r0,
+                                                  int64_t r1) {
+    const int64_t n = r1 - r0;
+    if constexpr (B::kXS) {
+      const int64_t nb = k / 256;
+      return Planes{rsrc(w + r0 * nb * 128, n * nb * 128), rsrc(w + n_rows * nb * 128 + r0 * nb * 8, n * nb * 8),
+                    static_cast<uint32_t>(nb)};
+    } else {
+      const int64_t nb = k / 32;
+      return Planes{rsrc(w + r0 * nb * 16, n * nb * 16), rsrc(w + n_rows * nb * 16 + r0 * nb * 2, n * nb * 2),
+                    static_cast<uint32_t>(nb)};
+    }
+  }
+  static __device__ __forceinline__ void bload(Payload& p, const Planes& P, bool none, uint32_t rr, uint32_t tb,
+                                               uint32_t lane, uint32_t lsk) {
+    if constexpr (B::kXS) {
+      p.q = bload16(rsrc_or_none(P.qs, none), (lane * 16u) | lsk, (rr * P.nb * 8u + tb) * 16u);
+      p.m = bload8(rsrc_or_none(P.d, none), ((lane >> 3) * 8u) | lsk, (rr * P.nb + (tb >> 3)) * 8u);
+      p.sub = static_cast<int>(lane & 7u);
+    } else {
+      const uint32_t b = rr * P.nb + tb;
+      p.q = bload16(rsrc_or_none(P.qs, none), (lane * 16u) | lsk, b * 16u);
+      p.m = make_uint2(bload2(rsrc_or_none(P.d, none), (lane * 2u) | lsk, b * 2u), 0u);
+      p.sub = 0;
+    }
+  }
   using XS = PlainX<32>;
   static constexpr int kE = XS::kE;
   using X = typename XS::X;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return XS::lds_bytes(k); }
   static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) { XS::xload(x, lds, T, t); }
   static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) { XS::stage(x, k, lds); }
-  static __device__ __forceinline__ float dot(const typename B::Payload& p, const X& x) {
-    const float s = B::kXS ? iq4xs_scale(p.m, p.sub) : fp16_ieee(p.m.x);
-    const float c = -1152.0f * s;
+  struct S {
+    float s, c;
+  };
+  static __device__ __forceinline__ S scale(const Payload& p, bool&) {
+    const float sc = B::kXS ? iq4xs_scale(p.m, p.sub) : fp16_ieee(p.m.x);
+    return S{sc, -1152.0f * sc};
+  }
+  static __device__ __forceinline__ S scale_rule(const Payload& p) {
+    bool unused = false;
+    return scale(p, unused);
+  }
+  static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
     const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
-    float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t lo = iq4_lut(w[i] & 0x0F0F0F0Fu), hi = iq4_lut((w[i] >> 4) & 0x0F0F0F0Fu);
       const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
-      s0 = dot2(wpair<kHi1024, kSel01>(lo, s, c), (i & 1) ? el.z : el.x, s0);
-      s1 = dot2(wpair<kHi1024, kSel23>(lo, s, c), (i & 1) ? el.w : el.y, s1);
-      s0 = dot2(wpair<kHi1024, kSel01>(hi, s, c), (i & 1) ? eh.z : eh.x, s0);
-      s1 = dot2(wpair<kHi1024, kSel23>(hi, s, c), (i & 1) ? eh.w : eh.y, s1);
+      a0 = dot2(wpair<kHi1024, kSel01>(lo, s.s, s.c), (i & 1) ? el.z : el.x, a0);
+      a1 = dot2(wpair<kHi1024, kSel23>(lo, s.s, s.c), (i & 1) ? el.w : el.y, a1);
+      a0 = dot2(wpair<kHi1024, kSel01>(hi, s.s, s.c), (i & 1) ? eh.z : eh.x, a0);
+      a1 = dot2(wpair<kHi1024, kSel23>(hi, s.s, s.c), (i & 1) ? eh.w : eh.y, a1);
     }
-    return s0 + s1;
   }
 };
 template <>
@@ -850,12 +1086,13 @@ __device__ __forceinline__ void store_y(void* y, int64_t r, float v) {
     static_cast<__bf16*>(y)[r] = static_cast<__bf16>(v);
 }
 
-// F: the format's arithmetic (Exact<TYPE> or the relaxed Fmt<TYPE>).
+// The relaxed kernel. F: the format's relaxed arithmetic (Fmt<TYPE>).
 // XREG: the row fits one pass (T <= 64 J) and each lane keeps the x of its J
 // tasks in registers. MASK: some tasks of a pass fall past the row's end.
 // DEPTH: units whose payload is in flight at once (a ring of DEPTH buffers).
-template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT>
-__global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
+// MINW: waves per SIMD the registers must allow (1: no cap).
+template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT, int MINW = 1>
+__global__ void __launch_bounds__(64 * WAVES, MINW) gemv_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
                                                           int64_t k, const uint16_t* __restrict__ x,
                                                           void* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -931,33 +1168,192 @@ __global__ void __launch_bounds__(64 * WAVES) gemv_kernel(const uint8_t* __restr
   }
 }
 
-template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK>
+// ---- the exact kernel -----------------------------------------------------------
+// The same work split and unit ring as gemv_kernel, with a branch-free memory
+// skeleton: payload loads, ring refills and y stores are buffer accesses
+// that every lane issues on every step. A task past the row's end (bit 31 of
+// the lane's offset), a unit past the wave's last (a buffer of no records)
+// and a lane with nothing to store (bit 31) access nothing; skipped loads
+// return zeros, so a masked task's weights are zero. With no memory access
+// under a branch, the compiler waits for exactly the oldest ring slot
+// instead of draining every load in flight each step. Offsets split into a
+// per-lane part, fixed for the wave, and the row and pass, in a scalar
+// register, so a refill costs no vector instructions.
+
+template <class F, int J, bool MASK>
+__device__ __forceinline__ void bload_unit(Unit<F, J>& U, const typename F::Planes& P, bool none, int rr, int pass,
+                                           int T, int lane) {
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int tb = pass * 64 * J + 64 * j;
+    const uint32_t lsk = (MASK && tb + lane >= T) ? kSkip : 0u;
+    F::bload(U.p[j], P, none, static_cast<uint32_t>(rr), static_cast<uint32_t>(tb), static_cast<uint32_t>(lane), lsk);
+  }
+}
+
+template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT, int MINW>
+__global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
+                                                                      int64_t k, const uint16_t* __restrict__ x,
+                                                                      void* __restrict__ y) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int kEsize = F32_OUT ? 4 : 2;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave =
+      static_cast<int64_t>(blockIdx.x) * WAVES + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int64_t n_waves = static_cast<int64_t>(gridDim.x) * WAVES;
+  const int64_t r0 = wave * n_rows / n_waves, r1 = (wave + 1) * n_rows / n_waves;
+  const int T = static_cast<int>(k / F::kTaskElems);
+  const int passes = XREG ? 1 : (T + 64 * J - 1) / (64 * J);
+  const int units = static_cast<int>(r1 - r0) * passes;
+  const typename F::Planes P = F::planes(w, n_rows, k, r0, r1);
+  const __amdgpu_buffer_rsrc_t Y = rsrc(static_cast<uint8_t*>(y) + r0 * kEsize, (r1 - r0) * kEsize);
+
+  // Unit coordinates (row relative to r0, pass) advance one pass at a time:
+  // (rl, pl) for loads, (rc, pc) for compute.
+  Unit<F, J> buf[DEPTH];
+  int rl = 0, pl = 0;
+  auto advance = [&](int& r, int& pass) {
+    if (++pass == passes) { pass = 0; ++r; }
+  };
+  // Issued slot by slot in the loop's order, so that the loop header sees
+  // the same sequence of loads in flight from the prologue as from the loop.
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    bload_unit<F, J, MASK>(buf[d], P, d >= units, rl, pl, T, lane);
+    advance(rl, pl);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  F::stage(x, k, lds);
+  __syncthreads();
+
+  typename F::X xr[XREG ? J : 1];
+  if constexpr (XREG) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int t = 64 * j + lane;
+      F::xload(xr[j], lds, T, t < T ? t : 0);
+    }
+  }
+
+  int rc = 0, pc = 0;
+  float a0 = 0.0f, a1 = 0.0f;
+  auto compute = [&](const Unit<F, J>& U) {
+    // The unit's scale terms first: the hardware conversion, and the
+    // reference's rule for every lane when any lane of the wave holds a
+    // special scale (a wave-uniform branch around arithmetic only).
+    typename F::S sc[J];
+    bool special = false;
+#pragma unroll
+    for (int j = 0; j < J; ++j) sc[j] = F::scale(U.p[j], special);
+    if constexpr (F::kRule) {
+      if (__builtin_amdgcn_ballot_w64(special) != 0) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) sc[j] = F::scale_rule(U.p[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      if constexpr (XREG) {
+        F::dot(U.p[j], xr[j], sc[j], a0, a1);
+      } else {
+        const int t = pc * 64 * J + 64 * j + lane;
+        typename F::X xt;
+        F::xload(xt, lds, T, t < T ? t : 0);
+        F::dot(U.p[j], xt, sc[j], a0, a1);
+      }
+    }
+    const bool end = XREG || pc == passes - 1;
+    float v = 0.0f;
+    if (end) {
+      v = wave_sum_last(a0 + a1);
+      a0 = a1 = 0.0f;
+    }
+    const uint32_t off = static_cast<uint32_t>(rc * kEsize) | ((lane == 63 && end) ? 0u : kSkip);
+    if constexpr (F32_OUT)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), Y, off, 0, 0);
+    else
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, static_cast<__bf16>(v)), Y, off, 0, 0);
+    advance(rc, pc);
+  };
+
+  // Scheduling barriers keep each slot's compute apart from the refills and
+  // the next slot: an instruction of the next slot hoisted into this one
+  // would make the compiler wait for that slot's loads early.
+  int u = 0;
+  for (; u + DEPTH <= units; u += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      compute(buf[d]);
+      __builtin_amdgcn_sched_barrier(0);
+      bload_unit<F, J, MASK>(buf[d], P, u + d + DEPTH >= units, rl, pl, T, lane);
+      advance(rl, pl);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DEPTH - 1; ++d)
+    if (u + d < units) compute(buf[d]);
+}
+
+template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, int MINW>
+int launch_exact_cfg(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  const int64_t lds = F::lds_bytes(k);
+  const void* kern = y_type == SPIRAL_TYPE_F32
+                         ? reinterpret_cast<const void*>(gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, true, MINW>)
+                         : reinterpret_cast<const void*>(gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, false, MINW>);
+  const int64_t resident = static_cast<int64_t>(device_cu_count()) * blocks_per_cu(kern, 64 * WAVES, lds);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n_rows, WAVES), resident));
+  // A wave's rows of a plane (at most one byte per element) must stay below
+  // 2 GiB: bit 31 of an offset marks a skipped access.
+  if (ceil_div(n_rows, blocks * WAVES) * k >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
+  const uint8_t* W = static_cast<const uint8_t*>(w);
+  if (y_type == SPIRAL_TYPE_F32)
+    hipLaunchKernelGGL((gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, true, MINW>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(64 * WAVES), lds, s, W, n_rows, k, x, y);
+  else
+    hipLaunchKernelGGL((gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, false, MINW>),
+                       dim3(static_cast<unsigned>(blocks)), dim3(64 * WAVES), lds, s, W, n_rows, k, x, y);
+  return launch_status();
+}
+
+template <class F, int J, int WAVES, int DEPTH, int MINW = 1>
+int launch_exact_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  const int64_t T = k / F::kTaskElems;
+  const bool mask = T % (64 * J) != 0;
+  if (T <= 64 * J)
+    return mask ? launch_exact_cfg<F, J, WAVES, DEPTH, true, true, MINW>(w, n_rows, k, x, y, y_type, s)
+                : launch_exact_cfg<F, J, WAVES, DEPTH, true, false, MINW>(w, n_rows, k, x, y, y_type, s);
+  return mask ? launch_exact_cfg<F, J, WAVES, DEPTH, false, true, MINW>(w, n_rows, k, x, y, y_type, s)
+              : launch_exact_cfg<F, J, WAVES, DEPTH, false, false, MINW>(w, n_rows, k, x, y, y_type, s);
+}
+
+template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, int MINW = 1>
 int launch_cfg(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   const int64_t lds = F::lds_bytes(k);
   const void* kern = y_type == SPIRAL_TYPE_F32
-                         ? reinterpret_cast<const void*>(gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, true>)
-                         : reinterpret_cast<const void*>(gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, false>);
+                         ? reinterpret_cast<const void*>(gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, true, MINW>)
+                         : reinterpret_cast<const void*>(gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, false, MINW>);
   const int64_t resident = static_cast<int64_t>(device_cu_count()) * blocks_per_cu(kern, 64 * WAVES, lds);
   const unsigned blocks = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n_rows, WAVES), resident)));
   const uint8_t* W = static_cast<const uint8_t*>(w);
   if (y_type == SPIRAL_TYPE_F32)
-    hipLaunchKernelGGL((gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, true>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
-                       n_rows, k, x, y);
+    hipLaunchKernelGGL((gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, true, MINW>), dim3(blocks), dim3(64 * WAVES), lds,
+                       s, W, n_rows, k, x, y);
   else
-    hipLaunchKernelGGL((gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, false>), dim3(blocks), dim3(64 * WAVES), lds, s, W,
-                       n_rows, k, x, y);
+    hipLaunchKernelGGL((gemv_kernel<F, J, WAVES, DEPTH, XREG, MASK, false, MINW>), dim3(blocks), dim3(64 * WAVES), lds,
+                       s, W, n_rows, k, x, y);
   return launch_status();
 }
 
-template <class F, int J, int WAVES, int DEPTH>
+template <class F, int J, int WAVES, int DEPTH, int MINW = 1>
 int launch_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   const int64_t T = k / F::kTaskElems;
   const bool xreg = T <= 64 * J, mask = T % (64 * J) != 0;
   if (xreg)
-    return mask ? launch_cfg<F, J, WAVES, DEPTH, true, true>(w, n_rows, k, x, y, y_type, s)
-                : launch_cfg<F, J, WAVES, DEPTH, true, false>(w, n_rows, k, x, y, y_type, s);
-  return mask ? launch_cfg<F, J, WAVES, DEPTH, false, true>(w, n_rows, k, x, y, y_type, s)
-              : launch_cfg<F, J, WAVES, DEPTH, false, false>(w, n_rows, k, x, y, y_type, s);
+    return mask ? launch_cfg<F, J, WAVES, DEPTH, true, true, MINW>(w, n_rows, k, x, y, y_type, s)
+                : launch_cfg<F, J, WAVES, DEPTH, true, false, MINW>(w, n_rows, k, x, y, y_type, s);
+  return mask ? launch_cfg<F, J, WAVES, DEPTH, false, true, MINW>(w, n_rows, k, x, y, y_type, s)
+              : launch_cfg<F, J, WAVES, DEPTH, false, false, MINW>(w, n_rows, k, x, y, y_type, s);
 }
 
 // Relaxed mode. J = tasks per lane per unit, chosen so that rows of up to
@@ -989,10 +1385,10 @@ template <int TYPE>
 int launch_exact(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   using F = Exact<TYPE>;
   const int64_t T = k / F::kTaskElems;
-  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 64) return launch_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 128) return launch_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  return launch_j<F, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_exact_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 64) return launch_exact_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T <= 128) return launch_exact_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  return launch_exact_j<F, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
 }
 
 template <int TYPE>
