@@ -61,7 +61,9 @@ typedef enum spiral_op {
   SPIRAL_OP_RESHAPE = 5,
   SPIRAL_OP_PERMUTE = 6,
   SPIRAL_OP_TRANSPOSE = 7,
-  SPIRAL_OP_GLU = 8 /* op_params[0]: SPIRAL_GLU_* variant, op_params[1]: swapped;
+  SPIRAL_OP_GLU = 8 /* op_params[0]: SPIRAL_GLU_* variant, op_params[1]: swapped
+                      (single-tensor form only: the split form, src1 set,
+                      activates src0 whatever it holds, as ggml does);
                       SWIGLU_OAI: op_params[2] alpha, [3] limit (floats) */
 } spiral_op;
 

@@ -336,7 +336,9 @@ int compute_mul_mat_id_glu(spiral_backend* be, const spiral_tensor* t, const spi
 }
 
 // GLU over rows of src0, or of src0 and src1 (split form); contiguous outer
-// dimensions, checked by supports_op.
+// dimensions, checked by supports_op. As in ggml, op_params[1] (swapped)
+// applies to the single-tensor form only: the split form always activates
+// src0 (ggml_glu_split sets it to 0, and ggml's kernels ignore it there).
 int compute_glu(spiral_backend* be, const spiral_tensor* t) {
   const spiral_tensor* a = t->src[0];
   const spiral_tensor* b2 = t->src[1];
@@ -347,7 +349,7 @@ int compute_glu(spiral_backend* be, const spiral_tensor* t) {
     std::memcpy(&alpha, &t->op_params[2], sizeof alpha);
     std::memcpy(&limit, &t->op_params[3], sizeof limit);
     if (b2 != nullptr)
-      return spiral_glu_split_swiglu_oai(t->op_params[1], alpha, limit, static_cast<const float*>(a->data),
+      return spiral_glu_split_swiglu_oai(0, alpha, limit, static_cast<const float*>(a->data),
                                          static_cast<int64_t>(a->nb[1] / 4), static_cast<const float*>(b2->data),
                                          static_cast<int64_t>(b2->nb[1] / 4), t->ne[0], rows,
                                          static_cast<float*>(t->data), static_cast<int64_t>(t->nb[1] / 4), be->stream);
@@ -356,7 +358,7 @@ int compute_glu(spiral_backend* be, const spiral_tensor* t) {
                                  static_cast<int64_t>(t->nb[1] / 4), be->stream);
   }
   if (b2 != nullptr)
-    return spiral_glu_split(t->op_params[0], t->op_params[1], static_cast<const float*>(a->data),
+    return spiral_glu_split(t->op_params[0], 0, static_cast<const float*>(a->data),
                             static_cast<int64_t>(a->nb[1] / 4), static_cast<const float*>(b2->data),
                             static_cast<int64_t>(b2->nb[1] / 4), t->ne[0], rows, static_cast<float*>(t->data),
                             static_cast<int64_t>(t->nb[1] / 4), be->stream);
@@ -366,7 +368,8 @@ int compute_glu(spiral_backend* be, const spiral_tensor* t) {
 }
 
 // ggml's split form fused: MUL_MAT_ID over the gate experts (g->src[0]) and
-// over the up experts (g->src[1]), same activations and ids, then GLU g.
+// over the up experts (g->src[1]), same activations and ids, then GLU g
+// (the gate activated, whatever op_params[1] holds, as in compute_glu).
 int compute_mul_mat_id_glu_split(spiral_backend* be, const spiral_tensor* g) {
   const spiral_tensor* tg = g->src[0];
   const spiral_tensor* tu = g->src[1];
@@ -381,8 +384,8 @@ int compute_mul_mat_id_glu_split(spiral_backend* be, const spiral_tensor* g) {
   const int64_t wsb = spiral_mul_mat_id_workspace_bytes(a->ne[2], ids->ne[1], ids->ne[0]);
   return spiral_mul_mat_id_glu_split(a->type, a->data, tu->src[0]->data, static_cast<int64_t>(a->nb[2]), a->ne[2],
                                      a->ne[1], a->ne[0], x, b->ne[1], static_cast<const int32_t*>(ids->data),
-                                     ids->ne[1], ids->ne[0], g->op_params[0], g->op_params[1], g->data,
-                                     SPIRAL_TYPE_F32, be->scratch + xbytes, wsb, be->stream);
+                                     ids->ne[1], ids->ne[0], g->op_params[0], 0, g->data, SPIRAL_TYPE_F32,
+                                     be->scratch + xbytes, wsb, be->stream);
 }
 
 // Node i (MUL_MAT_ID) can run fused with node i + 1 (GLU over it): nothing

@@ -179,7 +179,8 @@ def glu(a, op=GLU_SWIGLU, swapped=False, name="glu", alpha=1.702, limit=7.0):
 
 def glu_split(a, b, op=GLU_SWIGLU, swapped=False, name="glu_split", alpha=1.702, limit=7.0):
     """ggml_glu_split(a, b, op) (split form): act(a) * b over equal shapes, F32;
-    SWIGLU_OAI as ggml_swiglu_oai(a, b, alpha, limit)."""
+    SWIGLU_OAI as ggml_swiglu_oai(a, b, alpha, limit). `swapped` only sets
+    op_params[1], which the split form ignores, as in ggml."""
     t = _node(TYPE_F32, list(a.ne), OP_GLU, [a, b], name)
     _glu_params(t, op, swapped, alpha, limit)
     return t

@@ -12,7 +12,11 @@
 //    the CPU baseline at ragged shapes with padded strides;
 //  - every argument check of the device entry points and of the ggml
 //    surface that returns before device work (null, misaligned, negative,
-//    overflowing sizes), and the size queries at extreme arguments.
+//    overflowing sizes), and the size queries at extreme arguments;
+//  - the llama.cpp shim's tensor conversion, restated from INTEGRATION.md
+//    over a minimal ggml_tensor, on storage filled with garbage first: a row
+//    view and a whole-expert view of a weight through spiral_supports_op
+//    (which reads view_src before any buffer check) and the size query.
 // Any sanitizer report aborts the program (-fno-sanitize-recover=all); a
 // failed expectation prints the case and makes the exit status nonzero.
 #include <cstdint>
@@ -374,6 +378,131 @@ void check_validation() {
   spiral_backend_free(nullptr);
 }
 
+
+// ---- the llama.cpp shim's conversion ----------------
+// A minimal ggml_tensor with the fields the shim reads (ggml.h's names).
+struct ggml_tensor_mock {
+  int type;
+  void* buffer;  // ggml_backend_buffer_t; the shim maps ->context, NULL here
+  int64_t ne[4];
+  size_t nb[4];
+  int op;
+  int32_t op_params[16];
+  int32_t flags;
+  ggml_tensor_mock* src[10];
+  ggml_tensor_mock* view_src;
+  size_t view_offs;
+  void* data;
+  char name[64];
+};
+
+struct shim_node {
+  spiral_tensor t, src[SPIRAL_MAX_SRC], owner, src_owner[SPIRAL_MAX_SRC];
+};
+
+void shim_copy_fields(const ggml_tensor_mock* t, spiral_tensor* s) {
+  std::memset(s, 0, sizeof(*s));
+  s->type = t->type;
+  s->buffer = nullptr;
+  for (int i = 0; i < 4; ++i) {
+    s->ne[i] = t->ne[i];
+    s->nb[i] = t->nb[i];
+  }
+  s->op = t->op;  // the mock carries spiral's op ids already
+  std::memcpy(s->op_params, t->op_params, sizeof(s->op_params));
+  s->flags = t->flags;
+  s->data = t->data;
+  s->view_offs = t->view_offs;
+  std::strncpy(s->name, t->name, SPIRAL_MAX_NAME - 1);
+}
+
+void shim_to_spiral1(const ggml_tensor_mock* t, spiral_tensor* s, spiral_tensor* owner) {
+  shim_copy_fields(t, s);
+  if (t->view_src) {
+    shim_copy_fields(t->view_src, owner);
+    s->view_src = owner;
+  }
+}
+
+void shim_to_spiral(const ggml_tensor_mock* t, shim_node* n) {
+  shim_to_spiral1(t, &n->t, &n->owner);
+  for (int i = 0; i < SPIRAL_MAX_SRC; ++i)
+    if (t->src[i]) {
+      shim_to_spiral1(t->src[i], &n->src[i], &n->src_owner[i]);
+      n->t.src[i] = &n->src[i];
+    }
+}
+
+ggml_tensor_mock mock_tensor(int type, int64_t ne0, int64_t ne1, int64_t ne2, size_t row_bytes, size_t elem,
+                             void* data, const char* name) {
+  ggml_tensor_mock t;
+  std::memset(&t, 0, sizeof(t));
+  t.type = type;
+  t.ne[0] = ne0;
+  t.ne[1] = ne1;
+  t.ne[2] = ne2;
+  t.ne[3] = 1;
+  t.nb[0] = elem;
+  t.nb[1] = row_bytes;
+  t.nb[2] = row_bytes * static_cast<size_t>(ne1);
+  t.nb[3] = t.nb[2] * static_cast<size_t>(ne2);
+  t.data = data;
+  std::strncpy(t.name, name, sizeof(t.name) - 1);
+  return t;
+}
+
+void check_shim() {
+  const int q = SPIRAL_TYPE_Q4_0;
+  const int64_t k = 256, rows = 64, experts = 4;
+  const size_t rb = static_cast<size_t>(spiral_row_bytes(q, k));
+  std::vector<uint8_t> weight(rb * rows * experts), act(4096), out(4096), idsb(256);
+  // The owner: an expert stack [experts][rows][k] of Q4_0.
+  ggml_tensor_mock w = mock_tensor(q, k, rows, experts, rb, 18, weight.data(), "blk.0.ffn_gate_exps.weight");
+  // A row view (rows 8..39 of expert 0) and a whole-expert view (expert 2).
+  ggml_tensor_mock rowv = mock_tensor(q, k, 32, 1, rb, 18, weight.data() + 8 * rb, "rows");
+  rowv.op = SPIRAL_OP_VIEW;
+  rowv.view_src = &w;
+  rowv.view_offs = 8 * rb;
+  ggml_tensor_mock expv = mock_tensor(q, k, rows, 1, rb, 18, weight.data() + 2 * rows * rb, "expert 2");
+  expv.op = SPIRAL_OP_VIEW;
+  expv.view_src = &w;
+  expv.view_offs = 2 * rows * rb;
+  ggml_tensor_mock x = mock_tensor(SPIRAL_TYPE_F32, k, 1, 1, k * 4, 4, act.data(), "x");
+  ggml_tensor_mock ids = mock_tensor(SPIRAL_TYPE_I32, 2, 1, 1, 8, 4, idsb.data(), "ids");
+
+  for (const ggml_tensor_mock* a : {&w, &rowv, &expv}) {
+    ggml_tensor_mock mm = mock_tensor(SPIRAL_TYPE_F32, a->ne[1], 1, 1, a->ne[1] * 4, 4, out.data(), "mul_mat");
+    mm.op = SPIRAL_OP_MUL_MAT;
+    mm.src[0] = const_cast<ggml_tensor_mock*>(a);
+    mm.src[1] = &x;
+    ggml_tensor_mock gr = mock_tensor(SPIRAL_TYPE_F32, k, 2, 1, k * 4, 4, out.data(), "get_rows");
+    gr.op = SPIRAL_OP_GET_ROWS;
+    gr.src[0] = const_cast<ggml_tensor_mock*>(a);
+    gr.src[1] = &ids;
+    for (ggml_tensor_mock* node : {&mm, &gr}) {
+      // Storage as a caller's stack would leave it: garbage, then the shim.
+      shim_node* n = static_cast<shim_node*>(std::malloc(sizeof(shim_node)));
+      std::memset(n, 0xA5, sizeof(shim_node));
+      shim_to_spiral(node, n);
+      EXPECT(n->t.src[0] == &n->src[0] && n->t.src[1] == &n->src[1] && n->t.src[2] == nullptr, "shim srcs");
+      EXPECT(n->t.view_src == nullptr, "shim node view_src");
+      if (a->view_src) {
+        EXPECT(n->src[0].view_src == &n->src_owner[0] && n->src[0].view_offs == a->view_offs, "shim view mapped");
+        EXPECT(n->src_owner[0].data == weight.data() && n->src_owner[0].view_src == nullptr, "shim owner");
+      } else {
+        EXPECT(n->src[0].view_src == nullptr, "shim no view");
+      }
+      EXPECT(std::strcmp(n->src[0].name, a->name) == 0, "shim name");
+      // No buffer: the op is not supported, but supports_op reads every
+      // field (view_src included) without touching garbage.
+      EXPECT(spiral_supports_op(&n->t) == 0, "shim supports_op without a buffer");
+      EXPECT(spiral_buft_alloc_size(&n->src[0]) == static_cast<size_t>(a->ne[1] * a->ne[2]) * rb, "shim alloc_size");
+      EXPECT(spiral_buffer_init_tensor(nullptr, &n->src[0]) == SPIRAL_ERR_NULL, "shim init_tensor null buffer");
+      std::free(n);
+    }
+  }
+}
+
 }  // namespace
 
 int main() {
@@ -382,6 +511,8 @@ int main() {
   std::printf("repack checks done (%d failures so far)\n", g_failures);
   check_oracle();
   std::printf("oracle and CPU-baseline checks done (%d failures so far)\n", g_failures);
+  check_shim();
+  std::printf("shim checks done (%d failures so far)\n", g_failures);
   check_validation();
   std::printf("validation checks done: %d failures\n", g_failures);
   return g_failures == 0 ? 0 : 1;

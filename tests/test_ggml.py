@@ -429,6 +429,19 @@ def test_mul_mat_id_then_swiglu_oai(cuda):
     be.synchronize()
     ys = np.frombuffer(buf.get(gs), dtype=np.float32).reshape(n_tokens, top_k, F)
     assert ys.tobytes() == y.tobytes()  # same products, same GLU: the same bits
+    # ggml applies op_params[1] (swapped) to the single-tensor form only; a
+    # split node carrying 1 still activates src0 (the gate), here unfused
+    # (SWIGLU_OAI) and fused (SWIGLU over the two MUL_MAT_ID nodes).
+    gsw = buf.alloc(ggml.glu_split(pg, pu, ggml.GLU_SWIGLU_OAI, swapped=True, alpha=alpha, limit=limit))
+    assert be.graph_compute([pg, pu, gsw]) == 0
+    be.synchronize()
+    assert buf.get(gsw) == buf.get(gs)
+    g0 = buf.alloc(ggml.glu_split(pg, pu, ggml.GLU_SWIGLU))
+    g1 = buf.alloc(ggml.glu_split(pg, pu, ggml.GLU_SWIGLU, swapped=True))
+    assert be.graph_compute([pg, pu, g0]) == 0
+    assert be.graph_compute([pg, pu, g1]) == 0
+    be.synchronize()
+    assert buf.get(g1) == buf.get(g0)
     be.free()
     buf.free()
 
