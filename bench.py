@@ -179,13 +179,13 @@ def traffic_table():
 # workload -> (kernel-name fragments whose dispatches make one step, algorithmic
 # bytes of one step or None)
 TRAFFIC_KERNELS = {
-    "gemv_q8_0": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<8>,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
-    "gemv_q6_k": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<14>,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
-    "gemv_q4_0": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<2>,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
-    "gemv_q4_k": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<12>,"], 14336 * 4096 // 256 * 144 + 4096 * 2 + 14336 * 2),
-    "gemv_q5_k": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<13>,"], 14336 * 4096 // 256 * 176 + 4096 * 2 + 14336 * 2),
-    "gemv_iq4_nl": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<20>,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
-    "gemv_iq4_xs": (["gemv_kernel<spiral::(anonymousnamespace)::Exact<23>,"], 14336 * 4096 // 256 * 136 + 4096 * 2 + 14336 * 2),
+    "gemv_q8_0": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<8>,"], 14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
+    "gemv_q6_k": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<14>,"], 4096 * 14336 // 256 * 210 + 14336 * 2 + 4096 * 2),
+    "gemv_q4_0": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<2>,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "gemv_q4_k": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<12>,"], 14336 * 4096 // 256 * 144 + 4096 * 2 + 14336 * 2),
+    "gemv_q5_k": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<13>,"], 14336 * 4096 // 256 * 176 + 4096 * 2 + 14336 * 2),
+    "gemv_iq4_nl": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<20>,"], 14336 * 4096 // 32 * 18 + 4096 * 2 + 14336 * 2),
+    "gemv_iq4_xs": (["gemv_exact_kernel<spiral::(anonymousnamespace)::Exact<23>,"], 14336 * 4096 // 256 * 136 + 4096 * 2 + 14336 * 2),
     "gemv_relaxed_q8_0": (["gemv_kernel<spiral::(anonymousnamespace)::Fmt<8>,"],
                           14336 * 4096 // 32 * 34 + 4096 * 2 + 14336 * 2),
     "mul_mat_q4_0_m4": (["skinny_kernel<2,"], 14336 * 4096 // 32 * 18 + 4 * 4096 * 2 + 4 * 14336 * 2),
@@ -194,8 +194,8 @@ TRAFFIC_KERNELS = {
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
     "moe_q4_0": (["moe_stream_kernel<2,false,false,1,8>"], None),
     "moe_gate_up_swiglu_q4_0": (["moe_stream_kernel<2,false,true,1,8>"], None),
-    # prefill: gate_up in passes of 32 tokens, down in passes of 64
-    "moe_prefill_q4_0": (["moe_stream_kernel<2,false,false,2,12>", "moe_stream_kernel<2,false,false,4,12>"], None),
+    # prefill: the grouped-GEMM form (routing, packing of the routed rows, GEMM) for both stages
+    "moe_prefill_q4_0": (["route_kernel", "moe_pack_kernel<2>", "moe_gemm_kernel<2,false>"], None),
 }
 
 
@@ -232,7 +232,7 @@ def write_traffic(d):
                                 "write_scale": round(ws, 4)},
            "kernels": {}}
     for name, (frags, alg) in TRAFFIC_KERNELS.items():
-        launches = 2 if name == "moe_q4_0" else 1
+        launches = 2 if name in ("moe_q4_0", "moe_prefill_q4_0") else 1
         f = sum(pick(bf, fr) for fr in frags) * launches
         w = sum(pick(bw, fr) for fr in frags) * launches
         tb = (f * fs + w * ws) * 1024
@@ -607,8 +607,9 @@ def main():
             px2 = px2.view(pt, top_k, inter)
             py1 = torch.empty((pt, top_k, inter2), dtype=torch.bfloat16, device=dev)
             py2 = torch.empty((pt, top_k, hidden), dtype=torch.bfloat16, device=dev)
-            pws1 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev)
-            pws2 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev)
+            # workspaces for the grouped-GEMM form (routed rows packed per expert)
+            pws1 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev, TYPE_Q4_0, inter2, hidden)
+            pws2 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev, TYPE_Q4_0, hidden, inter)
 
             def launch_prefill(i):
                 c = i % copies

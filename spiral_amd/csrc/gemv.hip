@@ -167,7 +167,6 @@ constexpr int kStageUnroll = 4;
 // (128 + c) with v_perm they line up with consecutive x pairs.
 template <>
 struct Fmt<SPIRAL_TYPE_Q4_0> {
-  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 32, kE = 4;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 4); }
 
@@ -250,7 +249,6 @@ struct Fmt<SPIRAL_TYPE_Q4_0> {
 // x entries per task (half block): 4 x float4 = its 16 x. Sum: float.
 template <>
 struct Fmt<SPIRAL_TYPE_Q8_0> {
-  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 16, kE = 4;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 16) * (kE * 16 + 4); }
 
@@ -330,7 +328,6 @@ struct Fmt<SPIRAL_TYPE_Q8_0> {
 // group j at i / 8 * 8 .. + 7, in order. Sum: float4, one per group.
 template <>
 struct Fmt<SPIRAL_TYPE_Q6_K> {
-  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 64, kE = 8;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 64) * (kE * 16 + 16); }
 
@@ -454,7 +451,6 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
 //   sum_i x_i (d sc q_i - dmin m) = d sc (sum x (128 + q) - 128 sum x) - dmin m sum x
 template <int TYPE>
 struct FmtKQ {
-  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 32, kE = 4;
   static constexpr bool kQ5 = TYPE == SPIRAL_TYPE_Q5_K;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 8); }
@@ -568,7 +564,6 @@ struct Fmt<SPIRAL_TYPE_Q5_K> : FmtKQ<SPIRAL_TYPE_Q5_K> {};
 // qs dwords 0..3, entries 4..7 the high-nibble ones). Sum: float.
 template <int TYPE>
 struct FmtIQ4 {
-  static constexpr bool kExact = false;
   static constexpr int kTaskElems = 32, kE = 8;
   static constexpr bool kXS = TYPE == SPIRAL_TYPE_IQ4_XS;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * (kE * 16 + 4); }
@@ -736,7 +731,7 @@ __device__ __forceinline__ _Float16 bload_h(__amdgpu_buffer_rsrc_t r, uint32_t v
 // Both offset terms are exact in fp32 (129 * 8 d, 9 * 8 d).
 template <>
 struct Exact<SPIRAL_TYPE_Q4_0> : Fmt<SPIRAL_TYPE_Q4_0> {
-  static constexpr bool kExact = true, kRule = true;
+  static constexpr bool kRule = true;
   struct Planes {
     __amdgpu_buffer_rsrc_t qs, d;
     uint32_t nb;
@@ -781,7 +776,7 @@ struct Exact<SPIRAL_TYPE_Q4_0> : Fmt<SPIRAL_TYPE_Q4_0> {
 // Q8_0: q + 128 (q ^ 0x80) as fp16 1024 + q + 128, minus 1152 d (9 * 128 d).
 template <>
 struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
-  static constexpr bool kExact = true, kRule = true;
+  static constexpr bool kRule = true;
   struct Planes {
     __amdgpu_buffer_rsrc_t qs, d;
     uint32_t nb;
@@ -803,7 +798,6 @@ struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
     p.d = bload_h(rsrc_or_none(P.d, none), ((lane >> 1) * 2u) | lsk, (rr * P.nb + (tb >> 1)) * 2u);
   }
   using XS = PlainX<16>;
-  static constexpr int kE = XS::kE;
   using X = XS::X;
   static __host__ __device__ int64_t lds_bytes(int64_t k) { return XS::lds_bytes(k); }
   static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int T, int t) { XS::xload(x, lds, T, t); }
@@ -836,7 +830,7 @@ struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
 // so 1056 ds = 33 * 32 ds has at most 24 and is exact.
 template <>
 struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
-  static constexpr bool kExact = true, kRule = true;
+  static constexpr bool kRule = true;
   struct Planes {
     __amdgpu_buffer_rsrc_t ql, qh, sc, d;
     uint32_t nb;
@@ -925,7 +919,7 @@ struct ExactKQ : FmtKQ<TYPE> {
   using B = FmtKQ<TYPE>;
   using Payload = typename B::Payload;
   using X = typename B::X;
-  static constexpr bool kExact = true, kRule = false;
+  static constexpr bool kRule = false;
   struct Planes {
     __amdgpu_buffer_rsrc_t qs, qh, meta;
     uint32_t nb;
@@ -991,7 +985,7 @@ template <int TYPE>
 struct ExactIQ4 : FmtIQ4<TYPE> {
   using B = FmtIQ4<TYPE>;
   using Payload = typename B::Payload;
-  static constexpr bool kExact = true, kRule = false;
+  static constexpr bool kRule = false;
   struct Planes {
     __amdgpu_buffer_rsrc_t qs, d;
     uint32_t nb;

@@ -53,8 +53,19 @@
 
 #include "common.h"
 #include "dequant_impl.h"
+#include "moe_piece.h"
 
 namespace spiral {
+bool moe_gemm_fits(int type, int64_t n_expert, int64_t n_pairs, int64_t k);
+int64_t moe_gemm_extra_bytes(int64_t n_expert, int64_t n_pairs, int64_t k);
+int moe_gemm(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
+             const uint16_t* x, int64_t x_slots, int64_t top_k, int64_t n_pairs, const int32_t* offsets,
+             const int32_t* list, const int32_t* blk_base, const int32_t* mt_base, void* xp_ws, void* y,
+             int y_type, hipStream_t s);
+bool moe_grouped_shape(int type, int64_t n_expert, int64_t n_pairs, int64_t k);
+bool moe_grouped_fits(int type, int64_t n_expert, int64_t n_pairs, int64_t k, const void* x,
+                      int64_t workspace_bytes);
+
 namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -64,6 +75,29 @@ constexpr int kRouteThreads = 1024;
 constexpr int kRouteChunk = 4096;  // experts counted per LDS pass
 constexpr int kMoeBN = 64;  // weight rows per workgroup (16 per wave)
 
+// Exclusive prefix of v over the kRouteThreads threads of the workgroup
+// (block total in `total`). Every thread calls it; s_wave is free on entry
+// and on return.
+__device__ __forceinline__ int32_t block_exscan(int32_t v, int32_t* s_wave, int32_t& total, int lane, int wv) {
+  int32_t incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t u = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += u;
+  }
+  if (lane == 63) s_wave[wv] = incl;
+  __syncthreads();
+  int32_t wbase = 0;
+  total = 0;
+  for (int i = 0; i < kRouteThreads / 64; ++i) {
+    const int32_t u = s_wave[i];
+    wbase += i < wv ? u : 0;
+    total += u;
+  }
+  __syncthreads();
+  return wbase + incl - v;
+}
+
 // Workspace: offsets[n_expert + 1] then list[n_pairs] (int32).
 //
 // One workgroup: per chunk of kRouteChunk experts, count the pairs of each
@@ -71,11 +105,15 @@ constexpr int kMoeBN = 64;  // weight rows per workgroup (16 per wave)
 // scan, then scatter each pair's index into its expert's list. The order
 // inside a list is arbitrary; each output row is computed on its own, so it
 // does not change any result. Pairs with an id outside [0, n_expert) get a
-// zero output row.
+// zero output row. With blk_base set (the grouped-GEMM form), the same scan
+// also gives each expert's first 16-row block (blk_base) and first 128-row
+// m-tile (mt_base) in the packed layout, totals at [n_expert].
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __restrict__ ids, int32_t n_pairs,
                                                               int32_t n_expert, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ list, void* __restrict__ y,
-                                                              int64_t out_cols, int y_f32) {
+                                                              int64_t out_cols, int y_f32,
+                                                              int32_t* __restrict__ blk_base,
+                                                              int32_t* __restrict__ mt_base) {
   __shared__ int32_t s_cnt[kRouteChunk];
   __shared__ int32_t s_wave[kRouteThreads / 64];
   __shared__ int32_t s_bad[kRouteThreads];
@@ -87,7 +125,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
   // instead of one per id.
   constexpr int kRouteBatch = 8;
   if (tid == 0) s_nbad = 0;
-  int32_t base = 0;
+  int32_t base = 0, base16 = 0, base128 = 0;
   for (int32_t e0 = 0; e0 < n_expert; e0 += kRouteChunk) {
     const int32_t ne = min(kRouteChunk, n_expert - e0);
     for (int i = tid; i < kRouteChunk; i += kRouteThreads) s_cnt[i] = 0;
@@ -120,21 +158,31 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
       c[i] = s_cnt[kPer * tid + i];
       run += c[i];
     }
-    int32_t incl = run;
+    int32_t total = 0;
+    int32_t pos = base + block_exscan(run, s_wave, total, lane, wv);
+    if (blk_base != nullptr) {  // uniform
+      int32_t r16 = 0, r128 = 0;
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int32_t v = __shfl_up(incl, off, 64);
-      if (lane >= off) incl += v;
+      for (int i = 0; i < kPer; ++i) {
+        r16 += (c[i] + 15) >> 4;
+        r128 += (c[i] + 127) >> 7;
+      }
+      int32_t t16 = 0, t128 = 0;
+      int32_t p16 = base16 + block_exscan(r16, s_wave, t16, lane, wv);
+      int32_t p128 = base128 + block_exscan(r128, s_wave, t128, lane, wv);
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int e = kPer * tid + i;
+        if (e < ne) {
+          blk_base[e0 + e] = p16;
+          mt_base[e0 + e] = p128;
+        }
+        p16 += (c[i] + 15) >> 4;
+        p128 += (c[i] + 127) >> 7;
+      }
+      base16 += t16;
+      base128 += t128;
     }
-    if (lane == 63) s_wave[wv] = incl;
-    __syncthreads();
-    int32_t wbase = 0, total = 0;
-    for (int i = 0; i < kRouteThreads / 64; ++i) {
-      const int32_t v = s_wave[i];
-      wbase += i < wv ? v : 0;
-      total += v;
-    }
-    int32_t pos = base + wbase + incl - run;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int e = kPer * tid + i;
@@ -161,7 +209,13 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
     base += total;
     __syncthreads();
   }
-  if (tid == 0) offsets[n_expert] = base;
+  if (tid == 0) {
+    offsets[n_expert] = base;
+    if (blk_base != nullptr) {
+      blk_base[n_expert] = base16;
+      mt_base[n_expert] = base128;
+    }
+  }
   // Pairs routed nowhere produce a zero row, cleared by the whole workgroup.
   const auto clear_row = [&](int64_t row) {
     for (int64_t col = tid; col < out_cols; col += kRouteThreads) {
@@ -192,225 +246,6 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
   }
 }
 
-// One 128-wide k step of one weight row for lane group g (see the header):
-// loaded once, then dequantized 8 elements at a time for MFMA s = 0..3.
-// local(g, s, e) is the k offset inside the step of element e < 8 of MFMA s.
-template <int TYPE>
-struct MoePiece;
-
-// Q4_0: piece = block 4 kb + g. MFMA s takes qs dword s: its low nibbles
-// (elements 4s .. 4s + 3) then its high nibbles (16 + 4s .. 16 + 4s + 3).
-// A high nibble c is taken in place: byte 16 c under the high byte 0x54 is
-// the fp16 64 + c (exponent 6, mantissa step 1/16), and (64 + c) m - 72 m is
-// (c - 8) m, exact inside the FMA as (1024 + c) m - 1032 m is for the low
-// nibbles, with no shift.
-template <>
-struct MoePiece<SPIRAL_TYPE_Q4_0> {
-  uint4 q;
-  uint32_t d;
-  float m, off, off_hi;  // decoded scale and offsets (prep)
-  static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
-  __device__ __forceinline__ void prep() {
-    m = fp16_scale_fma(d);
-    off = -1032.0f * m;
-    off_hi = -72.0f * m;
-  }
-  // blk = block index of the lane's piece within the row's planar planes
-  __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t blk) {
-    q = *reinterpret_cast<const uint4*>(we + blk * 16);
-    d = *reinterpret_cast<const uint16_t*>(we + tot * 16 + blk * 2);
-  }
-  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
-  __device__ __forceinline__ uint4 dequant(int s) const {
-    const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
-    // all eight products first, then the packs: a pack right behind the FMA
-    // that feeds it costs a wait state
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = i ? hi : lo, magic = i ? 0x54545454u : 0x64646464u;
-      const float of = i ? off_hi : off;
-      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04010400u));
-      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04030402u));
-      v[4 * i] = __builtin_fmaf(static_cast<float>(a.x), m, of);
-      v[4 * i + 1] = __builtin_fmaf(static_cast<float>(a.y), m, of);
-      v[4 * i + 2] = __builtin_fmaf(static_cast<float>(b.x), m, of);
-      v[4 * i + 3] = __builtin_fmaf(static_cast<float>(b.y), m, of);
-    }
-    return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                      pack_bf16x2(v[6], v[7]));
-  }
-};
-
-// Q8_0: piece = block 4 kb + g; MFMA s takes qs bytes 8s .. 8s + 7.
-template <>
-struct MoePiece<SPIRAL_TYPE_Q8_0> {
-  uint4 q0, q1;
-  uint32_t d;
-  float m, off;  // decoded scale and offset (prep)
-  static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + 8 * s + e; }
-  __device__ __forceinline__ void prep() {
-    m = fp16_scale(d);
-    off = -1152.0f * m;
-  }
-  __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t blk) {
-    q0 = *reinterpret_cast<const uint4*>(we + blk * 32);
-    q1 = *reinterpret_cast<const uint4*>(we + blk * 32 + 16);
-    d = *reinterpret_cast<const uint16_t*>(we + tot * 32 + blk * 2);
-  }
-  __device__ __forceinline__ void zero() { q0 = q1 = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
-  __device__ __forceinline__ uint4 dequant(int s) const {
-    const uint32_t w0 = (s == 0 ? q0.x : s == 1 ? q0.z : s == 2 ? q1.x : q1.z) ^ 0x80808080u;
-    const uint32_t w1 = (s == 0 ? q0.y : s == 1 ? q0.w : s == 2 ? q1.y : q1.w) ^ 0x80808080u;
-    const float df = m;
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = i ? w1 : w0;
-      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
-      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), df, off), __builtin_fmaf(static_cast<float>(a.y), df, off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), df, off), __builtin_fmaf(static_cast<float>(b.y), df, off));
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
-  }
-};
-
-// Q6_K: a 128-wide step is half h of super-block sb; piece g = elements
-// 128 h + 32 g + l, l < 32 (ql[64 h + 32 (g & 1) + l] nibble g / 2, qh[32 h
-// + l] bits 2g, sub-scale sc[8 h + l / 16 + 2 g]); MFMA s takes l = 8s .. 8s+7.
-template <>
-struct MoePiece<SPIRAL_TYPE_Q6_K> {
-  uint4 l0, l1, h0, h1;
-  uint32_t ds2;  // fp16 d (bits 0..15), sc for l < 16 (16..23), sc for l >= 16 (24..31)
-  uint32_t sch;  // or-ed into ds2 bits 16..31 by prep (the streaming form loads it apart)
-  int ls, hs;
-  float m0, off0, m1, off1;  // d * sc and offsets for l < 16 and l >= 16 (prep)
-  __device__ __forceinline__ void prep() {
-    ds2 |= sch << 16;
-    const float d = fp16_scale(ds2 & 0xffffu);
-    m0 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 16));
-    m1 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 24));
-    off0 = -32.0f * m0;
-    off1 = -32.0f * m1;
-  }
-  static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + 8 * s + e; }
-  // sb_row = super-block index (row * nb + sb), h = half, g = group
-  __device__ __forceinline__ void load(const uint8_t* we, int64_t tot, int64_t sbi, int h, int g) {
-    const uint8_t* ql = we + sbi * 128 + 64 * h + 32 * (g & 1);
-    const uint8_t* qh = we + tot * 128 + sbi * 64 + 32 * h;
-    l0 = *reinterpret_cast<const uint4*>(ql);
-    l1 = *reinterpret_cast<const uint4*>(ql + 16);
-    h0 = *reinterpret_cast<const uint4*>(qh);
-    h1 = *reinterpret_cast<const uint4*>(qh + 16);
-    const uint32_t sc = *reinterpret_cast<const uint16_t*>(we + tot * 192 + sbi * 16 + 8 * h + 2 * g);
-    ds2 = *reinterpret_cast<const uint16_t*>(we + tot * 208 + sbi * 2) | (sc << 16);
-    sch = 0u;
-    ls = (g >> 1) * 4;
-    hs = 2 * g;
-  }
-  __device__ __forceinline__ void zero() { l0 = l1 = h0 = h1 = make_uint4(0u, 0u, 0u, 0u); ds2 = sch = 0u; ls = hs = 0; }
-  __device__ __forceinline__ uint4 dequant(int s) const {
-    const uint4 L = s < 2 ? l0 : l1, H = s < 2 ? h0 : h1;
-    const uint32_t wl0 = (s & 1) ? L.z : L.x, wl1 = (s & 1) ? L.w : L.y;
-    const uint32_t wh0 = (s & 1) ? H.z : H.x, wh1 = (s & 1) ? H.w : H.y;
-    const float ds = s < 2 ? m0 : m1;
-    const float off = s < 2 ? off0 : off1;
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = (((i ? wl1 : wl0) >> ls) & 0x0F0F0F0Fu) | ((((i ? wh1 : wh0) >> hs) & 0x03030303u) << 4);
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(c & 0xffu), ds, off),
-                             __builtin_fmaf(static_cast<float>((c >> 8) & 0xffu), ds, off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>((c >> 16) & 0xffu), ds, off),
-                                 __builtin_fmaf(static_cast<float>(c >> 24), ds, off));
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
-  }
-};
-
-// Q4_K / Q5_K: a 128-wide step is half h of super-block sb; piece g = qs
-// bytes 64 h + 32 (g / 2) + 16 (g % 2) .. + 15 of the super-block (chunk
-// c = 2 h + g / 2), both nibbles: MFMA s < 2 takes the low nibbles of bytes
-// 8 s .. 8 s + 7 (group 2 c), s >= 2 the high nibbles of bytes 8 (s - 2) ..
-// (group 2 c + 1); Q5_K adds bits 2 c / 2 c + 1 of the same positions of
-// qh[16 (g % 2) .. + 15]. The piece carries the super-block's meta entry.
-template <int TYPE>
-struct MoePieceKQ {
-  uint4 q, meta, qh;
-  int grp;                   // 2 c
-  float d0, m0, d1, m1;      // d * scale and -dmin * min of groups 2 c and 2 c + 1 (prep)
-  static __device__ __forceinline__ int local(int g, int s, int e) {
-    return 64 * (g >> 1) + (s < 2 ? 16 * (g & 1) + 8 * s : 32 + 16 * (g & 1) + 8 * (s - 2)) + e;
-  }
-  __device__ __forceinline__ void prep() {
-    const uint32_t sl = kq_scale_min(meta.y, meta.z, meta.w, grp);
-    const uint32_t sh = kq_scale_min(meta.y, meta.z, meta.w, grp + 1);
-    const float d = fp16_ieee(meta.x & 0xffffu), dm = fp16_ieee(meta.x >> 16);
-    d0 = d * static_cast<float>(sl & 0xffu);
-    m0 = -(dm * static_cast<float>(sl >> 8));
-    d1 = d * static_cast<float>(sh & 0xffu);
-    m1 = -(dm * static_cast<float>(sh >> 8));
-  }
-  __device__ __forceinline__ void zero() { q = meta = qh = make_uint4(0u, 0u, 0u, 0u); grp = 0; }
-  __device__ __forceinline__ uint4 dequant(int s) const {
-    const bool hi = s >= 2;
-    const uint32_t w0 = (s & 1) ? q.z : q.x, w1 = (s & 1) ? q.w : q.y;
-    const uint32_t h0 = (s & 1) ? qh.z : qh.x, h1 = (s & 1) ? qh.w : qh.y;
-    const float ds = hi ? d1 : d0, off = hi ? m1 : m0;
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      uint32_t c = ((i ? w1 : w0) >> (hi ? 4 : 0)) & 0x0F0F0F0Fu;
-      if constexpr (TYPE == SPIRAL_TYPE_Q5_K) c |= (((i ? h1 : h0) >> (grp + (hi ? 1 : 0))) & 0x01010101u) << 4;
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>(c & 0xffu), off),
-                             __builtin_fmaf(ds, static_cast<float>((c >> 8) & 0xffu), off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>((c >> 16) & 0xffu), off),
-                                 __builtin_fmaf(ds, static_cast<float>(c >> 24), off));
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
-  }
-};
-template <>
-struct MoePiece<SPIRAL_TYPE_Q4_K> : MoePieceKQ<SPIRAL_TYPE_Q4_K> {};
-template <>
-struct MoePiece<SPIRAL_TYPE_Q5_K> : MoePieceKQ<SPIRAL_TYPE_Q5_K> {};
-
-// IQ4_NL / IQ4_XS: piece g = 32 elements with one scale (IQ4_NL block 4 kb + g;
-// IQ4_XS sub-block 4 h + g of the step's super-block half h), 16 qs bytes:
-// MFMA s takes qs dword s, low nibbles (elements 4s .. 4s + 3) then high
-// nibbles (16 + 4s ..), as Q4_0; indices become codebook values (iq4_lut).
-template <int TYPE>
-struct MoePieceIQ4 {
-  uint4 q;
-  uint2 meta;  // IQ4_NL: fp16 d in meta.x; IQ4_XS: d, scales_h, scales_l
-  int sub;     // IQ4_XS sub-block
-  float m, off;
-  static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
-  __device__ __forceinline__ void prep() {
-    m = TYPE == SPIRAL_TYPE_IQ4_XS ? iq4xs_scale(meta, sub) : fp16_ieee(meta.x & 0xffffu);
-    off = -1152.0f * m;
-  }
-  __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); meta = make_uint2(0u, 0u); sub = 0; }
-  __device__ __forceinline__ uint4 dequant(int s) const {
-    const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = iq4_lut((i ? (w >> 4) : w) & 0x0F0F0F0Fu);
-      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
-      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), m, off), __builtin_fmaf(static_cast<float>(a.y), m, off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), m, off), __builtin_fmaf(static_cast<float>(b.y), m, off));
-    }
-    return make_uint4(o[0], o[1], o[2], o[3]);
-  }
-};
-template <>
-struct MoePiece<SPIRAL_TYPE_IQ4_NL> : MoePieceIQ4<SPIRAL_TYPE_IQ4_NL> {};
-template <>
-struct MoePiece<SPIRAL_TYPE_IQ4_XS> : MoePieceIQ4<SPIRAL_TYPE_IQ4_XS> {};
 
 constexpr int kMoeKC = 768;                   // k chunk of activations staged in LDS (3 pairs)
 constexpr int kMoeTok = 16;                   // tokens per pass (one MFMA row block)
@@ -932,118 +767,6 @@ constexpr int kStreamMinWaves = (TB == 1 && WAVES == 8 && TYPE != SPIRAL_TYPE_Q6
 template <int TYPE>
 constexpr int kStreamRing = TYPE == SPIRAL_TYPE_Q4_0 ? 4 : TYPE == SPIRAL_TYPE_Q8_0 ? 6 : 4;
 
-// A lane's piece offsets for one weight row (lane group g), and the loads
-// of k step st: the same pieces as WStage::piece reads from LDS.
-template <int TYPE>
-struct PieceAddr;
-
-template <>
-struct PieceAddr<SPIRAL_TYPE_Q4_0> {
-  uint32_t q, d;
-  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g) {
-    q = static_cast<uint32_t>((row * nb + g) * 16);
-    d = static_cast<uint32_t>((row * nb + g) * 2);
-  }
-  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_Q4_0>& pc, const Planes& P, int64_t st) const {
-    pc.q = bload16(P.a, q, static_cast<uint32_t>(st) * 64u);
-    pc.d = bload2(P.d, d, static_cast<uint32_t>(st) * 8u);
-  }
-};
-
-template <>
-struct PieceAddr<SPIRAL_TYPE_Q8_0> {
-  uint32_t q, d;
-  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g) {
-    q = static_cast<uint32_t>((row * nb + g) * 32);
-    d = static_cast<uint32_t>((row * nb + g) * 2);
-  }
-  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_Q8_0>& pc, const Planes& P, int64_t st) const {
-    pc.q0 = bload16(P.a, q, static_cast<uint32_t>(st) * 128u);
-    pc.q1 = bload16(P.a, q + 16u, static_cast<uint32_t>(st) * 128u);
-    pc.d = bload2(P.d, d, static_cast<uint32_t>(st) * 8u);
-  }
-};
-
-template <>
-struct PieceAddr<SPIRAL_TYPE_Q6_K> {
-  uint32_t l, h, sc, d;
-  int g;
-  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g_) {
-    g = g_;
-    l = static_cast<uint32_t>(row * nb * 128 + 32 * (g & 1));
-    h = static_cast<uint32_t>(row * nb * 64);
-    sc = static_cast<uint32_t>(row * nb * 16 + 2 * g);
-    d = static_cast<uint32_t>(row * nb * 2);
-  }
-  // Step st is half st % 2 of super-block st / 2.
-  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_Q6_K>& pc, const Planes& P, int64_t st) const {
-    const uint32_t sb = static_cast<uint32_t>(st >> 1), hh = static_cast<uint32_t>(st & 1);
-    pc.l0 = bload16(P.a, l, sb * 128u + 64u * hh);
-    pc.l1 = bload16(P.a, l + 16u, sb * 128u + 64u * hh);
-    pc.h0 = bload16(P.b, h, sb * 64u + 32u * hh);
-    pc.h1 = bload16(P.b, h + 16u, sb * 64u + 32u * hh);
-    pc.sch = bload2(P.c, sc, sb * 16u + 8u * hh);
-    pc.ds2 = bload2(P.d, d, sb * 2u);
-    pc.ls = (g >> 1) * 4;
-    pc.hs = 2 * g;
-  }
-};
-
-template <int TYPE>
-struct PieceAddrKQ {
-  uint32_t q, qh, meta;
-  int g;
-  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g_) {
-    g = g_;
-    q = static_cast<uint32_t>(row * nb * 128 + 32 * (g >> 1) + 16 * (g & 1));
-    qh = static_cast<uint32_t>(row * nb * 32 + 16 * (g & 1));
-    meta = static_cast<uint32_t>(row * nb * 16);
-  }
-  // Step st is half st % 2 of super-block st / 2.
-  __device__ __forceinline__ void load(MoePiece<TYPE>& pc, const Planes& P, int64_t st) const {
-    const uint32_t sb = static_cast<uint32_t>(st >> 1), hh = static_cast<uint32_t>(st & 1);
-    pc.q = bload16(P.a, q, sb * 128u + 64u * hh);
-    pc.meta = bload16(P.c, meta, sb * 16u);
-    if constexpr (TYPE == SPIRAL_TYPE_Q5_K) pc.qh = bload16(P.b, qh, sb * 32u);
-    pc.grp = 4 * static_cast<int>(hh) + 2 * (g >> 1);
-  }
-};
-template <>
-struct PieceAddr<SPIRAL_TYPE_Q4_K> : PieceAddrKQ<SPIRAL_TYPE_Q4_K> {};
-template <>
-struct PieceAddr<SPIRAL_TYPE_Q5_K> : PieceAddrKQ<SPIRAL_TYPE_Q5_K> {};
-
-template <>
-struct PieceAddr<SPIRAL_TYPE_IQ4_NL> {
-  uint32_t q, d;
-  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g) {
-    q = static_cast<uint32_t>((row * nb + g) * 16);
-    d = static_cast<uint32_t>((row * nb + g) * 2);
-  }
-  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_IQ4_NL>& pc, const Planes& P, int64_t st) const {
-    pc.q = bload16(P.a, q, static_cast<uint32_t>(st) * 64u);
-    pc.meta = make_uint2(bload2(P.d, d, static_cast<uint32_t>(st) * 8u), 0u);
-    pc.sub = 0;
-  }
-};
-
-template <>
-struct PieceAddr<SPIRAL_TYPE_IQ4_XS> {
-  uint32_t q, meta;
-  int g;
-  __device__ __forceinline__ void set(int64_t row, int64_t nb, int g_) {
-    g = g_;
-    q = static_cast<uint32_t>(row * nb * 128 + 16 * g);
-    meta = static_cast<uint32_t>(row * nb * 8);
-  }
-  // Step st is half st % 2 of super-block st / 2: sub-block 4 (st % 2) + g.
-  __device__ __forceinline__ void load(MoePiece<SPIRAL_TYPE_IQ4_XS>& pc, const Planes& P, int64_t st) const {
-    const uint32_t sb = static_cast<uint32_t>(st >> 1), hh = static_cast<uint32_t>(st & 1);
-    pc.q = bload16(P.a, q, sb * 128u + 64u * hh);
-    pc.meta = make_uint2(bload4(P.c, meta, sb * 8u), bload4(P.c, meta + 4u, sb * 8u));
-    pc.sub = 4 * static_cast<int>(hh) + g;
-  }
-};
 
 // What one ring slot of the streaming form holds (a "unit"), loaded for one
 // 16-row group of the wave. Q4_0: a pair of k steps of all 16 rows, loaded
@@ -1793,6 +1516,31 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
 
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_expert + 1 + n_pairs); }
 
+// Workspace with which a MUL_MAT_ID of this shape takes the grouped-GEMM
+// form (moe_workspace_bytes() when the shape does not qualify).
+int64_t moe_workspace_bytes_grouped(int type, int64_t n_expert, int64_t n_pairs, int64_t k) {
+  const int64_t base = moe_workspace_bytes(n_expert, n_pairs);
+  if (!moe_grouped_shape(type, n_expert, n_pairs, k)) return base;
+  return base + moe_gemm_extra_bytes(n_expert, n_pairs, k);
+}
+
+// Batches of at least this many (token, slot) pairs an expert on average
+// take the grouped-GEMM form (when the caller's workspace allows). At 64 an
+// expert (1024 tokens, top-8 over 128 experts) it measured level with the
+// streaming form's passes of 32 / 64 tokens (gate_up 169 against 171 us)
+// and slower for k = 768 (102 against 86 us).
+constexpr int64_t kGroupedMinAvg = 96;
+
+bool moe_grouped_shape(int type, int64_t n_expert, int64_t n_pairs, int64_t k) {
+  return n_pairs > kFusedPairs && n_pairs >= kGroupedMinAvg * n_expert && moe_gemm_fits(type, n_expert, n_pairs, k);
+}
+
+bool moe_grouped_fits(int type, int64_t n_expert, int64_t n_pairs, int64_t k, const void* x,
+                      int64_t workspace_bytes) {
+  return moe_grouped_shape(type, n_expert, n_pairs, k) && aligned16(x) &&
+         workspace_bytes >= moe_workspace_bytes_grouped(type, n_expert, n_pairs, k);
+}
+
 // Whether the fused GLU form (streaming kernel only) takes rows of k elements.
 bool moe_glu_fits_k(int64_t k) { return stream_lds_bytes(k) > 0; }
 
@@ -1839,7 +1587,8 @@ void* moe_static_scratch(int& rc) {
 // form), the F rows of w and of w_up, both at expert_stride.
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up) {
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up,
+        int64_t workspace_bytes) {
   const int64_t n_pairs = n_tokens * top_k;
   const int f32 = y_type == SPIRAL_TYPE_F32;
   const bool glu = glu_op >= 0;
@@ -1849,12 +1598,27 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   if (glu && stream_lds_bytes(k) == 0) return SPIRAL_ERR_SHAPE;
   int32_t* offsets = nullptr;
   int32_t* list = nullptr;
+  // The grouped-GEMM form (prefill-sized batches, workspace for the packed
+  // rows): its block and m-tile bases follow the lists in the workspace.
+  const bool grouped = !glu && moe_grouped_fits(type, n_expert, n_pairs, k, x, workspace_bytes);
+  int32_t* blk_base = nullptr;
+  int32_t* mt_base = nullptr;
   if (n_pairs > kFusedPairs) {
     offsets = static_cast<int32_t*>(workspace);
     list = offsets + n_expert + 1;
+    if (grouped) {
+      blk_base = list + n_pairs;
+      mt_base = blk_base + n_expert + 1;
+    }
     hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
-                       static_cast<int32_t>(n_expert), offsets, list, y, glu ? n_rows / 2 : n_rows, f32);
+                       static_cast<int32_t>(n_expert), offsets, list, y, glu ? n_rows / 2 : n_rows, f32, blk_base,
+                       mt_base);
     if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
+  }
+  if (grouped) {
+    const uintptr_t xp = (reinterpret_cast<uintptr_t>(mt_base + n_expert + 1) + 255) & ~uintptr_t(255);
+    return moe_gemm(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, top_k, n_pairs, offsets, list, blk_base,
+                    mt_base, reinterpret_cast<void*>(xp), y, y_type, s);
   }
   if (stream_lds_bytes(k) > 0) {
 #define SPIRAL_MOE_STREAM_AS(T, F, G) \
