@@ -194,8 +194,8 @@ TRAFFIC_KERNELS = {
     "gemm_q4_0": (["pack_x_kernel", "gemm_kernel<2,"], 4096 * 4096 // 32 * 18 + 2 * (512 * 4096 * 2)),
     "moe_q4_0": (["moe_stream_kernel<2,false,false,1,8>"], None),
     "moe_gate_up_swiglu_q4_0": (["moe_stream_kernel<2,false,true,1,8>"], None),
-    # prefill: the grouped-GEMM form (routing, packing of the routed rows, GEMM) for both stages
-    "moe_prefill_q4_0": (["route_kernel", "moe_pack_kernel<2>", "moe_gemm_kernel<2,false>"], None),
+    # prefill (64 pairs an expert: the streaming form): gate_up in passes of 32 tokens, down in passes of 64
+    "moe_prefill_q4_0": (["moe_stream_kernel<2,false,false,2,12>", "moe_stream_kernel<2,false,false,4,12>"], None),
 }
 
 
@@ -232,7 +232,7 @@ def write_traffic(d):
                                 "write_scale": round(ws, 4)},
            "kernels": {}}
     for name, (frags, alg) in TRAFFIC_KERNELS.items():
-        launches = 2 if name in ("moe_q4_0", "moe_prefill_q4_0") else 1
+        launches = 2 if name == "moe_q4_0" else 1
         f = sum(pick(bf, fr) for fr in frags) * launches
         w = sum(pick(bw, fr) for fr in frags) * launches
         tb = (f * fs + w * ws) * 1024

@@ -523,6 +523,10 @@ __device__ __forceinline__ void moe_stage(uint16_t* As, const uint16_t* __restri
         if (kb + k0 < k) lo[b] = *reinterpret_cast<const uint2*>(src + k0);
         if (kb + k4 < k) hi[b] = *reinterpret_cast<const uint2*>(src + k4);
       }
+      if constexpr (kStageSwap<TYPE>) {
+        lo[b] = stage_swap(lo[b]);
+        hi[b] = stage_swap(hi[b]);
+      }
     }
 #pragma unroll
     for (int b = 0; b < kStageBatch; ++b) {
@@ -940,6 +944,7 @@ __global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ list, void* __restrict__ y,
     int64_t rows_per_wg, int glu_op, int swapped, const uint8_t* __restrict__ w_up) {
   constexpr int kPass = kMoeTok * TB;  // tokens per pass
+  constexpr uint32_t kEsize = F32_OUT ? 4 : 2, kOutSkip = 0x80000000u;
   extern __shared__ __align__(16) uint16_t As[];  // kPass rows of `pitch` bf16
   __shared__ int32_t s_pair[kPass];
   __shared__ int64_t s_xrow[kPass];
@@ -950,6 +955,7 @@ __global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)
   const int32_t lane_z = static_cast<int32_t>(blockIdx.z), n_lanes_z = static_cast<int32_t>(gridDim.z);
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t feat = GLU ? n_rows / 2 : n_rows;  // output columns
+  const __amdgpu_buffer_rsrc_t Y = buffer_rsrc(y, static_cast<uint32_t>(static_cast<int64_t>(n_pairs) * feat * kEsize));
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg;
   const int64_t r1 = min(r0 + rows_per_wg, feat);
   int32_t begin, end;
@@ -1036,6 +1042,17 @@ __global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)
     const uint16_t* arow[TB];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb) arow[tb] = As + min(kMoeTok * tb + (lane & 15), nt - 1) * pitch + 8 * g;
+    // Output row offsets of the lane's four pairs per row block (bytes; the
+    // caller keeps y below 2 GiB): a pair that does not exist points past
+    // the buffer (bit 31), where the buffer store drops its value.
+    uint32_t yo[TB][4];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int32_t pr = s_pair[kMoeTok * tb + 4 * g + i];
+        yo[tb][i] = pr >= 0 ? static_cast<uint32_t>(pr) * static_cast<uint32_t>(feat) * kEsize : kOutSkip;
+      }
     f32x4_t acc[TB][4];
     f32x4_t gate[TB];  // GLU: the group's gate sums
 #pragma unroll
@@ -1082,8 +1099,10 @@ __global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)
         }
       } else if (cu == gunits) {
         // acc[tb]: lane l holds rows 16 tb + 4 (l / 16) + i (routed pairs) of
-        // column l % 16.
+        // column l % 16. Every lane stores (no branch around the stores):
+        // columns past the workgroup's range point past the buffer.
         const int64_t n = row_of(cj);
+        const uint32_t n_off = static_cast<uint32_t>(n) * kEsize, n_skip = n < r1 ? 0u : kOutSkip;
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
           f32x4_t sum = (acc[tb][0] + acc[tb][1]) + (acc[tb][2] + acc[tb][3]);
@@ -1094,13 +1113,12 @@ __global__ void __launch_bounds__(64 * WAVES, (kStreamMinWaves<TYPE, TB, WAVES>)
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int32_t pr = s_pair[kMoeTok * tb + 4 * g + i];
-            if (pr >= 0 && n < r1) {
-              if constexpr (F32_OUT)
-                static_cast<float*>(y)[pr * feat + n] = sum[i];
-              else
-                static_cast<__bf16*>(y)[pr * feat + n] = static_cast<__bf16>(sum[i]);
-            }
+            const uint32_t off = (yo[tb][i] + n_off) | n_skip;
+            if constexpr (F32_OUT)
+              __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum[i]), Y, off, 0, 0);
+            else
+              __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, static_cast<__bf16>(sum[i])), Y,
+                                                    off, 0, 0);
           }
 #pragma unroll
           for (int s = 0; s < 4; ++s) acc[tb][s] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -1582,9 +1600,10 @@ void* moe_static_scratch(int& rc) {
 
 // Arguments validated by the caller. glu_op < 0: plain MUL_MAT_ID; otherwise
 // the fused GLU form (n_rows = 2F even), which only the streaming form
-// implements (k <= kStreamMaxK, else SPIRAL_ERR_SHAPE): gate rows [0, F) and
-// up rows [F, 2F) of each expert matrix, or, with w_up set (ggml's split
-// form), the F rows of w and of w_up, both at expert_stride.
+// implements (k <= kStreamMaxK and y below 2 GiB, else SPIRAL_ERR_SHAPE):
+// gate rows [0, F) and up rows [F, 2F) of each expert matrix, or, with w_up
+// set (ggml's split form), the F rows of w and of w_up, both at
+// expert_stride.
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
         int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up,
@@ -1595,7 +1614,10 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   // Weight planes of one expert are addressed with 32-bit offsets.
   const int64_t wbytes = spiral_tensor_bytes(type, n_rows, k);
   if (wbytes == 0 || wbytes >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
-  if (glu && stream_lds_bytes(k) == 0) return SPIRAL_ERR_SHAPE;
+  // The streaming form writes y through a buffer resource (32-bit offsets).
+  const int64_t y_bytes = n_pairs * (glu ? n_rows / 2 : n_rows) * (f32 ? 4 : 2);
+  const bool stream_ok = stream_lds_bytes(k) > 0 && y_bytes < (int64_t(1) << 31);
+  if (glu && !stream_ok) return SPIRAL_ERR_SHAPE;
   int32_t* offsets = nullptr;
   int32_t* list = nullptr;
   // The grouped-GEMM form (prefill-sized batches, workspace for the packed
@@ -1620,7 +1642,7 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
     return moe_gemm(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, top_k, n_pairs, offsets, list, blk_base,
                     mt_base, reinterpret_cast<void*>(xp), y, y_type, s);
   }
-  if (stream_lds_bytes(k) > 0) {
+  if (stream_ok) {
 #define SPIRAL_MOE_STREAM_AS(T, F, G) \
   launch_stream<T, F, G>(w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_pairs, top_k, offsets, list, y, \
                          glu_op, swapped, w_up, s)

@@ -88,7 +88,11 @@ __global__ void __launch_bounds__(kGPackThreads) moe_pack_kernel(const uint16_t*
       if (b == a + 4) {
         v = *reinterpret_cast<const uint4*>(src + a);
       } else {
-        const uint2 lo = *reinterpret_cast<const uint2*>(src + a), hi = *reinterpret_cast<const uint2*>(src + b);
+        uint2 lo = *reinterpret_cast<const uint2*>(src + a), hi = *reinterpret_cast<const uint2*>(src + b);
+        if constexpr (kStageSwap<TYPE>) {
+          lo = stage_swap(lo);
+          hi = stage_swap(hi);
+        }
         v = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
     }

@@ -20,18 +20,35 @@ namespace {
 template <int TYPE>
 struct MoePiece;
 
-// Q4_0: piece = block 4 kb + g. MFMA s takes qs dword s: its low nibbles
-// (elements 4s .. 4s + 3) then its high nibbles (16 + 4s .. 16 + 4s + 3).
-// A high nibble c is taken in place: byte 16 c under the high byte 0x54 is
-// the fp16 64 + c (exponent 6, mantissa step 1/16), and (64 + c) m - 72 m is
-// (c - 8) m, exact inside the FMA as (1024 + c) m - 1032 m is for the low
-// nibbles, with no shift.
+// Whether MFMA s's elements e = 0..3 (and 4..7) are the four consecutive
+// elements local(g, s, 0) + {0, 2, 1, 3}: the activations of each run of
+// four are then staged with the middle two swapped (stage_swap).
+template <int TYPE>
+constexpr bool kStageSwap = TYPE == SPIRAL_TYPE_Q4_0;
+
+// (a0, a1, a2, a3) -> (a0, a2, a1, a3) for four bf16 in two dwords.
+__device__ __forceinline__ uint2 stage_swap(uint2 v) {
+  return make_uint2(__builtin_amdgcn_perm(v.y, v.x, 0x05040100u), __builtin_amdgcn_perm(v.y, v.x, 0x07060302u));
+}
+
+// Q4_0: piece = block 4 kb + g. MFMA s takes qs dword s: bytes j = 0..3
+// hold elements 4s + j (low nibbles) and 16 + 4s + j (high nibbles). One
+// v_and_or_b32 turns two nibbles into an fp16 pair in place: (w & 0x000F000F)
+// | 0x64006400 is (1024 + c) for elements 4s and 4s + 2, (w & 0x00F000F0) |
+// 0x54005400 is (64 + c) for 16 + 4s and 16 + 4s + 2 (byte 16 c under the
+// high byte 0x54: exponent 6, mantissa step 1/16), and w >> 8 gives the odd
+// elements the same way. (1024 + c) m - 1032 m and (64 + c) m - 72 m are
+// (c - 8) m, exact inside the FMA. So MFMA s takes elements 4s, 4s + 2,
+// 4s + 1, 4s + 3, then the same plus 16: the activations are staged in that
+// order (kStageSwap).
 template <>
 struct MoePiece<SPIRAL_TYPE_Q4_0> {
   uint4 q;
   uint32_t d;
   float m, off, off_hi;  // decoded scale and offsets (prep)
-  static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + (e < 4 ? 4 * s + e : 12 + 4 * s + e); }
+  static __device__ __forceinline__ int local(int g, int s, int e) {
+    return 32 * g + (e >= 4 ? 16 : 0) + 4 * s + ((e & 1) << 1) + ((e >> 1) & 1);
+  }
   __device__ __forceinline__ void prep() {
     m = fp16_scale_fma(d);
     off = -1032.0f * m;
@@ -43,22 +60,29 @@ struct MoePiece<SPIRAL_TYPE_Q4_0> {
     d = *reinterpret_cast<const uint16_t*>(we + tot * 16 + blk * 2);
   }
   __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
+  // v_and_or_b32 with the mask in an SGPR and the high bytes in a VGPR (a
+  // gfx9 VOP3 reads one scalar operand and no literal; written out, the
+  // compiler would emit a v_and and a v_or with literals instead).
+  static __device__ __forceinline__ f16x2_t and_or(uint32_t w, uint32_t mask, uint32_t hi) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(hi));
+    return __builtin_bit_cast(f16x2_t, r);
+  }
   __device__ __forceinline__ uint4 dequant(int s) const {
     const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
+    const uint32_t w8 = w >> 8;
+    const f16x2_t p[4] = {and_or(w, 0x000F000Fu, 0x64006400u),    // 4s, 4s + 2
+                          and_or(w8, 0x000F000Fu, 0x64006400u),   // 4s + 1, 4s + 3
+                          and_or(w, 0x00F000F0u, 0x54005400u),    // 16 + (4s, 4s + 2)
+                          and_or(w8, 0x00F000F0u, 0x54005400u)};  // 16 + (4s + 1, 4s + 3)
     // all eight products first, then the packs: a pack right behind the FMA
     // that feeds it costs a wait state
     float v[8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = i ? hi : lo, magic = i ? 0x54545454u : 0x64646464u;
-      const float of = i ? off_hi : off;
-      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04010400u));
-      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(magic, c, 0x04030402u));
-      v[4 * i] = __builtin_fmaf(static_cast<float>(a.x), m, of);
-      v[4 * i + 1] = __builtin_fmaf(static_cast<float>(a.y), m, of);
-      v[4 * i + 2] = __builtin_fmaf(static_cast<float>(b.x), m, of);
-      v[4 * i + 3] = __builtin_fmaf(static_cast<float>(b.y), m, of);
+    for (int i = 0; i < 4; ++i) {
+      const float of = i < 2 ? off : off_hi;
+      v[2 * i] = __builtin_fmaf(static_cast<float>(p[i].x), m, of);
+      v[2 * i + 1] = __builtin_fmaf(static_cast<float>(p[i].y), m, of);
     }
     return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
                       pack_bf16x2(v[6], v[7]));
