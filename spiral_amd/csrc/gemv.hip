@@ -370,7 +370,8 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
     for (int i = 0; i < 8; ++i) x.x[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
     x.sum = reinterpret_cast<const float4*>(lds + pad64(T) * kE * 16)[u];
   }
-  // Item = (task, group): 16 x (2 x 16 B) and their sum.
+  // Item = (task, group): 16 x (2 x 16 B) and (SUMS) their sum.
+  template <bool SUMS = true>
   static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
     const int T = static_cast<int>(k / 64);
     float* xs = reinterpret_cast<float*>(lds + pad64(T) * kE * 16);
@@ -398,11 +399,12 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const uint4 q = v[u][i];
-          s += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
-               (bf16_lo(q.w) + bf16_hi(q.w));
+          if constexpr (SUMS)
+            s += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
+                 (bf16_lo(q.w) + bf16_hi(q.w));
           *reinterpret_cast<uint4*>(dst + 1024 * i) = q;
         }
-        xs[e] = s;
+        if constexpr (SUMS) xs[e] = s;
       }
     }
   }
@@ -485,7 +487,8 @@ struct FmtKQ {
     for (int i = 0; i < 4; ++i) x.xp[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
     x.sum = reinterpret_cast<const float2*>(lds + pad64(T) * kE * 16)[t];
   }
-  // Item = task: 2 x 16 x (2 x 16 B) and the two sums.
+  // Item = task: 2 x 16 x (2 x 16 B) and (SUMS) the two sums.
+  template <bool SUMS = true>
   static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
     const int T = static_cast<int>(k / 32);
     float2* xs = reinterpret_cast<float2*>(lds + pad64(T) * kE * 16);
@@ -511,11 +514,12 @@ struct FmtKQ {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint4 q = v[u][i];
-          s[i >> 1] += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
-                       (bf16_lo(q.w) + bf16_hi(q.w));
+          if constexpr (SUMS)
+            s[i >> 1] += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) +
+                         (bf16_lo(q.z) + bf16_hi(q.z)) + (bf16_lo(q.w) + bf16_hi(q.w));
           *reinterpret_cast<uint4*>(dst + 1024 * i) = q;
         }
-        xs[b] = make_float2(s[0], s[1]);
+        if constexpr (SUMS) xs[b] = make_float2(s[0], s[1]);
       }
     }
   }
@@ -831,6 +835,16 @@ struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
 template <>
 struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
   static constexpr bool kRule = true;
+  // The relaxed form's staging without the group sums: the exact products
+  // take the -32 offset inside each weight.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    Fmt<SPIRAL_TYPE_Q6_K>::stage<false>(x, k, lds);
+  }
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int, int u) {
+    const uint8_t* e = lds + lds_task(u, kE);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x.x[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+  }
   struct Planes {
     __amdgpu_buffer_rsrc_t ql, qh, sc, d;
     uint32_t nb;
@@ -920,6 +934,16 @@ struct ExactKQ : FmtKQ<TYPE> {
   using Payload = typename B::Payload;
   using X = typename B::X;
   static constexpr bool kRule = false;
+  // The relaxed form's staging without the sums: -dmin * min is inside each
+  // weight here.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    B::template stage<false>(x, k, lds);
+  }
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int, int t) {
+    const uint8_t* e = lds + lds_task(t, B::kE);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x.xp[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+  }
   struct Planes {
     __amdgpu_buffer_rsrc_t qs, qh, meta;
     uint32_t nb;
