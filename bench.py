@@ -607,15 +607,13 @@ def main():
             px2 = px2.view(pt, top_k, inter)
             py1 = torch.empty((pt, top_k, inter2), dtype=torch.bfloat16, device=dev)
             py2 = torch.empty((pt, top_k, hidden), dtype=torch.bfloat16, device=dev)
-            # workspaces for the grouped-GEMM form (routed rows packed per expert)
-            pws1 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev, TYPE_Q4_0, inter2, hidden)
-            pws2 = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev, TYPE_Q4_0, hidden, inter)
+            pws = ops.mul_mat_id_workspace(n_expert, pt, top_k, dev)  # the routing lists
 
             def launch_prefill(i):
                 c = i % copies
-                ops.mul_mat_id(TYPE_Q4_0, gus[c], gu_per, n_expert, inter2, hidden, px1, pids_d, workspace=pws1,
+                ops.mul_mat_id(TYPE_Q4_0, gus[c], gu_per, n_expert, inter2, hidden, px1, pids_d, workspace=pws,
                                out=py1)
-                ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, px2, pids_d, workspace=pws2,
+                ops.mul_mat_id(TYPE_Q4_0, dns[c], dn_per, n_expert, hidden, inter, px2, pids_d, workspace=pws,
                                out=py2)
 
             issue, ev = timer.run(launch_prefill, steps, warmup)

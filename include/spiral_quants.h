@@ -227,20 +227,6 @@ int spiral_gemv_relaxed(int type, const void* w, int64_t n_rows, int64_t k,
  *     for the per-expert token lists (caller-owned, no allocation here). */
 int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens,
                                           int64_t top_k);
-/* Workspace with which spiral_mul_mat_id takes its grouped-GEMM form, for
- * prefill-sized batches (at least 96 (token, slot) pairs an expert on
- * average, more than 1024 pairs, k a multiple of 128, x 16-byte aligned):
- * the routing lists, then the routed activation rows gathered per expert
- * into MFMA operand order (about (n_tokens * top_k + 15 n_expert) * k * 2
- * bytes). Equal to spiral_mul_mat_id_workspace_bytes() for shapes that do
- * not qualify. Any workspace of at least the minimum works: a smaller one
- * keeps the streaming form. Both forms give the same results, bit for bit
- * (each (pair, row) sum is formed from the same operands in the same
- * order). No counterpart in the reference (its MoE path is CPU code). */
-int64_t spiral_mul_mat_id_workspace_bytes_grouped(int type, int64_t n_expert,
-                                                  int64_t n_rows, int64_t k,
-                                                  int64_t n_tokens,
-                                                  int64_t top_k);
 int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride,
                       int64_t n_expert, int64_t n_rows, int64_t k,
                       const uint16_t* x, int64_t x_slots, const int32_t* ids,

@@ -55,7 +55,6 @@ SIGNATURES = {
     "spiral_gemv_relaxed_max_k": (_i64, [_int]),
     "spiral_gemv_relaxed": (_int, [_int, _p, _i64, _i64, _p, _p, _int, _p]),
     "spiral_mul_mat_id_workspace_bytes": (_i64, [_i64, _i64, _i64]),
-    "spiral_mul_mat_id_workspace_bytes_grouped": (_i64, [_int, _i64, _i64, _i64, _i64, _i64]),
     "spiral_mul_mat_id": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,
                                  _p, _i64, _p]),
     "spiral_mul_mat_id_noalloc": (_int, [_int, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _int,

@@ -15,11 +15,9 @@ bool skinny_fits(int type, int64_t n_rows, int64_t k, int64_t m);
 int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x, int64_t ldx, int64_t m, void* y,
            int y_type, int64_t ldy, hipStream_t s);
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs);
-int64_t moe_workspace_bytes_grouped(int type, int64_t n_expert, int64_t n_pairs, int64_t k);
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up = nullptr,
-        int64_t workspace_bytes = 0);
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up = nullptr);
 int glu(int op, int swapped, const float* x, int64_t ldx, int64_t n, int64_t rows, float* y, int64_t ldy,
         hipStream_t s, float alpha, float limit);
 int glu_split(int op, int swapped, const float* xg, int64_t ldg, const float* xu, int64_t ldu, int64_t n,
@@ -119,13 +117,6 @@ int64_t spiral_mul_mat_id_workspace_bytes(int64_t n_expert, int64_t n_tokens, in
   return moe_workspace_bytes(n_expert, pairs);
 }
 
-int64_t spiral_mul_mat_id_workspace_bytes_grouped(int type, int64_t n_expert, int64_t n_rows, int64_t k,
-                                                  int64_t n_tokens, int64_t top_k) {
-  const int64_t base = spiral_mul_mat_id_workspace_bytes(n_expert, n_tokens, top_k);
-  if (base == 0 || !is_quant_type(type) || n_rows <= 0 || k <= 0 || k % block_elems(type) != 0) return base;
-  return moe_workspace_bytes_grouped(type, n_expert, n_tokens * top_k, k);
-}
-
 int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,
                       int64_t k, const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens,
                       int64_t top_k, void* y, int y_type, void* workspace, int64_t workspace_bytes,
@@ -138,7 +129,7 @@ int spiral_mul_mat_id(int type, const void* w, int64_t expert_stride, int64_t n_
   rc = require_device();
   if (rc != SPIRAL_OK) return rc;
   return moe(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, ids, n_tokens, top_k, y, y_type, -1, 0,
-             workspace, static_cast<hipStream_t>(stream), nullptr, workspace_bytes);
+             workspace, static_cast<hipStream_t>(stream));
 }
 
 int spiral_mul_mat_id_noalloc(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows,

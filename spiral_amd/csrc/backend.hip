@@ -211,21 +211,15 @@ size_t mul_mat_workspace(const spiral_tensor* t) {
   return align_up(static_cast<size_t>(n > 0 ? n : 0), kAlign);
 }
 
-// Workspace of a MUL_MAT_ID node: enough for its grouped-GEMM form at
-// prefill sizes (the minimum, the routing lists, otherwise).
-int64_t mul_mat_id_workspace(const spiral_tensor* t) {
-  const spiral_tensor* a = t->src[0];
-  const spiral_tensor* ids = t->src[2];
-  return spiral_mul_mat_id_workspace_bytes_grouped(a->type, a->ne[2], a->ne[1], a->ne[0], ids->ne[1], ids->ne[0]);
-}
-
 size_t node_scratch(const spiral_tensor* t) {
   switch (t->op) {
     case SPIRAL_OP_MUL_MAT: return act_scratch(t->src[1]) + mul_mat_workspace(t);
     case SPIRAL_OP_MUL_MAT_ID: {
       const spiral_tensor* b = t->src[1];
+      const spiral_tensor* ids = t->src[2];
       size_t need = align_up(static_cast<size_t>(b->ne[0] * b->ne[1] * b->ne[2]) * 2, kAlign);
-      need += align_up(static_cast<size_t>(mul_mat_id_workspace(t)), kAlign);
+      need += align_up(static_cast<size_t>(spiral_mul_mat_id_workspace_bytes(t->src[0]->ne[2], ids->ne[1], ids->ne[0])),
+                       kAlign);
       return need;
     }
     default: return 0;
@@ -317,7 +311,7 @@ int compute_mul_mat_id(spiral_backend* be, const spiral_tensor* t) {
   const uint16_t* x = act_bf16(b, be->scratch, true, be->stream, ld1, ld2, ld3, rc);
   if (rc != SPIRAL_OK) return rc;
   const size_t xbytes = align_up(static_cast<size_t>(b->ne[0] * b->ne[1] * b->ne[2]) * 2, kAlign);
-  const int64_t wsb = mul_mat_id_workspace(t);
+  const int64_t wsb = spiral_mul_mat_id_workspace_bytes(a->ne[2], ids->ne[1], ids->ne[0]);
   return spiral_mul_mat_id(a->type, a->data, static_cast<int64_t>(a->nb[2]), a->ne[2], a->ne[1], a->ne[0], x,
                            b->ne[1], static_cast<const int32_t*>(ids->data), ids->ne[1], ids->ne[0], t->data,
                            SPIRAL_TYPE_F32, be->scratch + xbytes, wsb, be->stream);

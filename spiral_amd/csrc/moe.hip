@@ -56,16 +56,6 @@
 #include "moe_piece.h"
 
 namespace spiral {
-bool moe_gemm_fits(int type, int64_t n_expert, int64_t n_pairs, int64_t k);
-int64_t moe_gemm_extra_bytes(int64_t n_expert, int64_t n_pairs, int64_t k);
-int moe_gemm(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
-             const uint16_t* x, int64_t x_slots, int64_t top_k, int64_t n_pairs, const int32_t* offsets,
-             const int32_t* list, const int32_t* blk_base, const int32_t* mt_base, void* xp_ws, void* y,
-             int y_type, hipStream_t s);
-bool moe_grouped_shape(int type, int64_t n_expert, int64_t n_pairs, int64_t k);
-bool moe_grouped_fits(int type, int64_t n_expert, int64_t n_pairs, int64_t k, const void* x,
-                      int64_t workspace_bytes);
-
 namespace {
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -75,29 +65,6 @@ constexpr int kRouteThreads = 1024;
 constexpr int kRouteChunk = 4096;  // experts counted per LDS pass
 constexpr int kMoeBN = 64;  // weight rows per workgroup (16 per wave)
 
-// Exclusive prefix of v over the kRouteThreads threads of the workgroup
-// (block total in `total`). Every thread calls it; s_wave is free on entry
-// and on return.
-__device__ __forceinline__ int32_t block_exscan(int32_t v, int32_t* s_wave, int32_t& total, int lane, int wv) {
-  int32_t incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int32_t u = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += u;
-  }
-  if (lane == 63) s_wave[wv] = incl;
-  __syncthreads();
-  int32_t wbase = 0;
-  total = 0;
-  for (int i = 0; i < kRouteThreads / 64; ++i) {
-    const int32_t u = s_wave[i];
-    wbase += i < wv ? u : 0;
-    total += u;
-  }
-  __syncthreads();
-  return wbase + incl - v;
-}
-
 // Workspace: offsets[n_expert + 1] then list[n_pairs] (int32).
 //
 // One workgroup: per chunk of kRouteChunk experts, count the pairs of each
@@ -105,15 +72,11 @@ __device__ __forceinline__ int32_t block_exscan(int32_t v, int32_t* s_wave, int3
 // scan, then scatter each pair's index into its expert's list. The order
 // inside a list is arbitrary; each output row is computed on its own, so it
 // does not change any result. Pairs with an id outside [0, n_expert) get a
-// zero output row. With blk_base set (the grouped-GEMM form), the same scan
-// also gives each expert's first 16-row block (blk_base) and first 128-row
-// m-tile (mt_base) in the packed layout, totals at [n_expert].
+// zero output row.
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __restrict__ ids, int32_t n_pairs,
                                                               int32_t n_expert, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ list, void* __restrict__ y,
-                                                              int64_t out_cols, int y_f32,
-                                                              int32_t* __restrict__ blk_base,
-                                                              int32_t* __restrict__ mt_base) {
+                                                              int64_t out_cols, int y_f32) {
   __shared__ int32_t s_cnt[kRouteChunk];
   __shared__ int32_t s_wave[kRouteThreads / 64];
   __shared__ int32_t s_bad[kRouteThreads];
@@ -125,7 +88,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
   // instead of one per id.
   constexpr int kRouteBatch = 8;
   if (tid == 0) s_nbad = 0;
-  int32_t base = 0, base16 = 0, base128 = 0;
+  int32_t base = 0;
   for (int32_t e0 = 0; e0 < n_expert; e0 += kRouteChunk) {
     const int32_t ne = min(kRouteChunk, n_expert - e0);
     for (int i = tid; i < kRouteChunk; i += kRouteThreads) s_cnt[i] = 0;
@@ -158,31 +121,21 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
       c[i] = s_cnt[kPer * tid + i];
       run += c[i];
     }
-    int32_t total = 0;
-    int32_t pos = base + block_exscan(run, s_wave, total, lane, wv);
-    if (blk_base != nullptr) {  // uniform
-      int32_t r16 = 0, r128 = 0;
+    int32_t incl = run;
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        r16 += (c[i] + 15) >> 4;
-        r128 += (c[i] + 127) >> 7;
-      }
-      int32_t t16 = 0, t128 = 0;
-      int32_t p16 = base16 + block_exscan(r16, s_wave, t16, lane, wv);
-      int32_t p128 = base128 + block_exscan(r128, s_wave, t128, lane, wv);
-#pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const int e = kPer * tid + i;
-        if (e < ne) {
-          blk_base[e0 + e] = p16;
-          mt_base[e0 + e] = p128;
-        }
-        p16 += (c[i] + 15) >> 4;
-        p128 += (c[i] + 127) >> 7;
-      }
-      base16 += t16;
-      base128 += t128;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t v = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += v;
     }
+    if (lane == 63) s_wave[wv] = incl;
+    __syncthreads();
+    int32_t wbase = 0, total = 0;
+    for (int i = 0; i < kRouteThreads / 64; ++i) {
+      const int32_t v = s_wave[i];
+      wbase += i < wv ? v : 0;
+      total += v;
+    }
+    int32_t pos = base + wbase + incl - run;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int e = kPer * tid + i;
@@ -209,13 +162,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
     base += total;
     __syncthreads();
   }
-  if (tid == 0) {
-    offsets[n_expert] = base;
-    if (blk_base != nullptr) {
-      blk_base[n_expert] = base16;
-      mt_base[n_expert] = base128;
-    }
-  }
+  if (tid == 0) offsets[n_expert] = base;
   // Pairs routed nowhere produce a zero row, cleared by the whole workgroup.
   const auto clear_row = [&](int64_t row) {
     for (int64_t col = tid; col < out_cols; col += kRouteThreads) {
@@ -1534,31 +1481,6 @@ int skinny(int type, const void* w, int64_t n_rows, int64_t k, const uint16_t* x
 
 int64_t moe_workspace_bytes(int64_t n_expert, int64_t n_pairs) { return 4 * (n_expert + 1 + n_pairs); }
 
-// Workspace with which a MUL_MAT_ID of this shape takes the grouped-GEMM
-// form (moe_workspace_bytes() when the shape does not qualify).
-int64_t moe_workspace_bytes_grouped(int type, int64_t n_expert, int64_t n_pairs, int64_t k) {
-  const int64_t base = moe_workspace_bytes(n_expert, n_pairs);
-  if (!moe_grouped_shape(type, n_expert, n_pairs, k)) return base;
-  return base + moe_gemm_extra_bytes(n_expert, n_pairs, k);
-}
-
-// Batches of at least this many (token, slot) pairs an expert on average
-// take the grouped-GEMM form (when the caller's workspace allows). At 64 an
-// expert (1024 tokens, top-8 over 128 experts) it measured level with the
-// streaming form's passes of 32 / 64 tokens (gate_up 169 against 171 us)
-// and slower for k = 768 (102 against 86 us).
-constexpr int64_t kGroupedMinAvg = 96;
-
-bool moe_grouped_shape(int type, int64_t n_expert, int64_t n_pairs, int64_t k) {
-  return n_pairs > kFusedPairs && n_pairs >= kGroupedMinAvg * n_expert && moe_gemm_fits(type, n_expert, n_pairs, k);
-}
-
-bool moe_grouped_fits(int type, int64_t n_expert, int64_t n_pairs, int64_t k, const void* x,
-                      int64_t workspace_bytes) {
-  return moe_grouped_shape(type, n_expert, n_pairs, k) && aligned16(x) &&
-         workspace_bytes >= moe_workspace_bytes_grouped(type, n_expert, n_pairs, k);
-}
-
 // Whether the fused GLU form (streaming kernel only) takes rows of k elements.
 bool moe_glu_fits_k(int64_t k) { return stream_lds_bytes(k) > 0; }
 
@@ -1606,8 +1528,7 @@ void* moe_static_scratch(int& rc) {
 // expert_stride.
 int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_t n_rows, int64_t k,
         const uint16_t* x, int64_t x_slots, const int32_t* ids, int64_t n_tokens, int64_t top_k, void* y,
-        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up,
-        int64_t workspace_bytes) {
+        int y_type, int glu_op, int swapped, void* workspace, hipStream_t s, const void* w_up) {
   const int64_t n_pairs = n_tokens * top_k;
   const int f32 = y_type == SPIRAL_TYPE_F32;
   const bool glu = glu_op >= 0;
@@ -1620,27 +1541,12 @@ int moe(int type, const void* w, int64_t expert_stride, int64_t n_expert, int64_
   if (glu && !stream_ok) return SPIRAL_ERR_SHAPE;
   int32_t* offsets = nullptr;
   int32_t* list = nullptr;
-  // The grouped-GEMM form (prefill-sized batches, workspace for the packed
-  // rows): its block and m-tile bases follow the lists in the workspace.
-  const bool grouped = !glu && moe_grouped_fits(type, n_expert, n_pairs, k, x, workspace_bytes);
-  int32_t* blk_base = nullptr;
-  int32_t* mt_base = nullptr;
   if (n_pairs > kFusedPairs) {
     offsets = static_cast<int32_t*>(workspace);
     list = offsets + n_expert + 1;
-    if (grouped) {
-      blk_base = list + n_pairs;
-      mt_base = blk_base + n_expert + 1;
-    }
     hipLaunchKernelGGL(route_kernel, dim3(1), dim3(kRouteThreads), 0, s, ids, static_cast<int32_t>(n_pairs),
-                       static_cast<int32_t>(n_expert), offsets, list, y, glu ? n_rows / 2 : n_rows, f32, blk_base,
-                       mt_base);
+                       static_cast<int32_t>(n_expert), offsets, list, y, glu ? n_rows / 2 : n_rows, f32);
     if (hipGetLastError() != hipSuccess) return SPIRAL_ERR_HIP;
-  }
-  if (grouped) {
-    const uintptr_t xp = (reinterpret_cast<uintptr_t>(mt_base + n_expert + 1) + 255) & ~uintptr_t(255);
-    return moe_gemm(type, w, expert_stride, n_expert, n_rows, k, x, x_slots, top_k, n_pairs, offsets, list, blk_base,
-                    mt_base, reinterpret_cast<void*>(xp), y, y_type, s);
   }
   if (stream_ok) {
 #define SPIRAL_MOE_STREAM_AS(T, F, G) \

@@ -1,4 +1,4 @@
-// Per-format weight pieces of the MoE and grouped-GEMM kernels: one 128-wide
+// Per-format weight pieces of the MoE kernels: one 128-wide
 // k step of one weight row for MFMA lane group g, loaded once and
 // dequantized exactly to bf16 eight elements at a time, one group of eight
 // for each of the step's four v_mfma_f32_16x16x32_bf16 (MFMA s takes

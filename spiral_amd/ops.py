@@ -110,14 +110,8 @@ def gemv_relaxed(qtype, w, n_rows, k, x, out_dtype=torch.bfloat16, out=None):
     return out
 
 
-def mul_mat_id_workspace(n_expert, n_tokens, top_k, device, qtype=None, n_rows=None, k=None):
-    """Workspace for mul_mat_id: the minimum (routing lists), or, given the
-    weight format and shape, enough for the grouped-GEMM form that
-    prefill-sized batches take."""
-    if qtype is None:
-        n = lib().spiral_mul_mat_id_workspace_bytes(n_expert, n_tokens, top_k)
-    else:
-        n = lib().spiral_mul_mat_id_workspace_bytes_grouped(qtype, n_expert, n_rows, k, n_tokens, top_k)
+def mul_mat_id_workspace(n_expert, n_tokens, top_k, device):
+    n = lib().spiral_mul_mat_id_workspace_bytes(n_expert, n_tokens, top_k)
     return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
 
 
@@ -131,7 +125,7 @@ def mul_mat_id(qtype, w, expert_stride, n_expert, n_rows, k, x, ids, out_dtype=t
     ids = ids.to(torch.int32).contiguous()
     x = x.contiguous()
     if workspace is None:
-        workspace = mul_mat_id_workspace(n_expert, n_tokens, top_k, w.device, qtype, n_rows, k)
+        workspace = mul_mat_id_workspace(n_expert, n_tokens, top_k, w.device)
     if out is None:
         out = torch.empty((n_tokens, top_k, n_rows), dtype=out_dtype, device=w.device)
     check(lib().spiral_mul_mat_id(qtype, _ptr(w), expert_stride, n_expert, n_rows, k, _ptr(x), x_slots,

@@ -110,18 +110,6 @@ def test_sizes(spiral_lib):
     assert L.spiral_tensor_bytes(_lib.TYPE_Q6_K, 4096, 14336) == 48_168_960
     assert L.spiral_tensor_bytes(_lib.TYPE_Q4_0, 4096, 4096) == 9_437_184
     assert L.spiral_mul_mat_id_workspace_bytes(128, 64, 8) == 4 * (129 + 512)
-    # Grouped-GEMM form: the lists, block and m-tile bases, a 256-byte gap and
-    # the routed rows packed in 16-row blocks of k bf16; shapes that do not
-    # take it (decode sizes, k not a multiple of 128) need only the lists.
-    grouped = L.spiral_mul_mat_id_workspace_bytes_grouped
-    blocks = (16384 + 15 * 128) // 16 + 1
-    assert grouped(_lib.TYPE_Q4_0, 128, 1536, 2048, 2048, 8) == (4 * (129 + 16384) + 8 * 129 + 256
-                                                                 + blocks * 16 * 2048 * 2)
-    assert grouped(_lib.TYPE_Q4_0, 128, 1536, 2048, 64, 8) == 4 * (129 + 512)
-    assert grouped(_lib.TYPE_Q4_0, 128, 1536, 2048, 1024, 8) == 4 * (129 + 8192)  # 64 pairs an expert: streaming
-    assert grouped(_lib.TYPE_Q4_0, 128, 1536, 2080, 2048, 8) == 4 * (129 + 16384)
-    assert grouped(_lib.TYPE_Q6_K, 128, 1536, 100, 2048, 8) == 4 * (129 + 16384)  # k not a block multiple
-    assert grouped(_lib.TYPE_Q4_0, 0, 1536, 2048, 2048, 8) == 0  # a shape spiral_mul_mat_id refuses
     # GEMV (m = 1) and the small-batch form (m = 2..16) need no workspace; the
     # GEMM packs m rows (rounded up to 16) of k bf16
     assert L.spiral_mul_mat_workspace_bytes(_lib.TYPE_Q8_0, 14336, 4096, 1) == 0

@@ -1,21 +1,15 @@
 """GPU parity of MUL_MAT_ID at prefill sizes: many routed tokens per expert.
 
-Two forms take these batches. The streaming form runs passes of 32 or 64 of
-an expert's tokens (two or four MFMA row blocks per dequantized weight, as
-far as the activations of k fit in LDS), the passes of one expert on several
-workgroups side by side (pass lanes). The grouped-GEMM form (batches of more
-than 1024 pairs averaging at least 96 an expert, given the workspace
-spiral_mul_mat_id_workspace_bytes_grouped() asks for, which ops.mul_mat_id
-allocates) packs each expert's routed rows and multiplies 128-row m-tiles
-against 64-column n-tiles, dequantizing each weight once per m-tile.
-Covered: every format in both forms, each pass size at the k that limits it,
-m-tiles and n-tiles cut short, k of one and two steps, a skewed routing (one
-expert with hundreds of pairs), ids routed nowhere, per-slot inputs, bf16
-and float32 output, the fused GLU form. The product is the reference's
-(src/quants/tests/mmul.py:104-126), held to the bars of
+Passes then take 32 or 64 of an expert's tokens (two or four MFMA row blocks
+per dequantized weight, as far as the activations of k fit in LDS), and the
+passes of one expert run on several workgroups side by side (pass lanes).
+Covered: every format, each pass size at the k that limits it, a skewed
+routing (one expert with hundreds of pairs, several passes per lane), ids
+routed nowhere, bf16 and float32 output, the fused GLU form. The product is
+the reference's (src/quants/tests/mmul.py:104-126), held to the bars of
 tests/test_gpu_parity.py; each (pair, row) sum is formed exactly as in a
-decode-sized call in both forms, so a prefill call equals per-chunk decode
-calls, and the grouped form equals the streaming form, bit for bit.
+decode-sized call, so a prefill call also equals per-chunk decode calls bit
+for bit.
 """
 
 import numpy as np
@@ -125,60 +119,3 @@ def test_prefill_bench_shape_equals_decode_calls(cuda, stage):
                     for t, s in sel])
     got = np.stack([big[t, s].cpu().numpy() for t, s in sel])
     assert rel_err(got, ref) <= REL_TOL_EXACT_W
-
-
-def _both_forms(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, out_dtype, ids=None):
-    """The same MUL_MAT_ID through the grouped-GEMM form (its workspace) and
-    the streaming form (the minimum workspace)."""
-    w, per, raws, ids, x = _moe_inputs(cuda, qtype, n_expert, n, k, n_tokens, top_k, x_slots, seed, ids)
-    xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
-    ws_min = ops.mul_mat_id_workspace(n_expert, n_tokens, top_k, cuda)
-    ws_grp = ops.mul_mat_id_workspace(n_expert, n_tokens, top_k, cuda, qtype, n, k)
-    assert ws_grp.numel() > ws_min.numel()  # the shape takes the grouped form
-    grouped = ops.mul_mat_id(qtype, w, per, n_expert, n, k, xd, idd, out_dtype=out_dtype, workspace=ws_grp)
-    stream = ops.mul_mat_id(qtype, w, per, n_expert, n, k, xd, idd, out_dtype=out_dtype, workspace=ws_min)
-    torch.cuda.synchronize()
-    return grouped, stream, raws, ids, x
-
-
-@pytest.mark.parametrize("qtype", FORMATS)
-def test_grouped_every_format(cuda, qtype):
-    """600 tokens, top-2 over 8 experts (150 pairs an expert: an m-tile of
-    128 rows and one of 22), 104 rows (an n-tile cut short), k = 512: the
-    grouped form equals the streaming form bit for bit and the oracle within
-    the bars."""
-    n_expert, n, k, n_tokens, top_k = 8, 104, 512, 600, 2
-    g, st, raws, ids, x = _both_forms(cuda, qtype, n_expert, n, k, n_tokens, top_k, 1, 71, torch.float32)
-    assert torch.equal(g, st)
-    check_moe(g.cpu().numpy(), _moe_ref(qtype, raws, n, k, ids, x), True)
-
-
-@pytest.mark.parametrize("qtype,k", [(O.Q4_0, 128), (O.Q8_0, 256), (O.Q4_K, 256)])
-def test_grouped_short_rows(cuda, qtype, k):
-    """k of one or two 128-wide steps: an n-tile ends every unit or every
-    second one (1600 pairs over 16 experts, 200 rows)."""
-    n_expert, n, n_tokens, top_k = 16, 200, 800, 2
-    g, st, raws, ids, x = _both_forms(cuda, qtype, n_expert, n, k, n_tokens, top_k, 1, 72, torch.float32)
-    assert torch.equal(g, st)
-    check_moe(g.cpu().numpy(), _moe_ref(qtype, raws, n, k, ids, x), True)
-
-
-def test_grouped_skew_bad_ids_per_slot(cuda):
-    """1600 pairs over 12 experts, expert 5 taking 600 of them (five m-tiles),
-    ids routed nowhere (zero rows), per-slot inputs, k = 768 (six steps, not a
-    multiple of the four-unit loop), 200 rows; bf16 and float32 output."""
-    n_expert, n, k, n_tokens, top_k = 12, 200, 768, 800, 2
-    rng = np.random.default_rng(73)
-    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
-    ids[:600, 0] = 5
-    ids[:600, 1] = np.where(ids[:600, 1] == 5, 6, ids[:600, 1])
-    ids[::11, 1] = -1
-    ids[3::19, 0] = 77
-    for out_dtype in (torch.float32, torch.bfloat16):
-        g, st, raws, ids_used, x = _both_forms(cuda, O.Q4_0, n_expert, n, k, n_tokens, top_k, 2, 74, out_dtype,
-                                               ids=ids)
-        assert torch.equal(g, st)
-        gy = g.float().cpu().numpy()
-        bad = (ids_used < 0) | (ids_used >= n_expert)
-        assert not gy[bad].any()
-        check_moe(gy, _moe_ref(O.Q4_0, raws, n, k, ids_used, x), out_dtype == torch.float32)
