@@ -63,6 +63,7 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteChunk = 4096;  // experts counted per LDS pass
+constexpr int kRouteLdsList = 8192;  // lists of up to this many pairs are built in LDS
 constexpr int kMoeBN = 64;  // weight rows per workgroup (16 per wave)
 
 // Workspace: offsets[n_expert + 1] then list[n_pairs] (int32).
@@ -72,7 +73,9 @@ constexpr int kMoeBN = 64;  // weight rows per workgroup (16 per wave)
 // scan, then scatter each pair's index into its expert's list. The order
 // inside a list is arbitrary; each output row is computed on its own, so it
 // does not change any result. Pairs with an id outside [0, n_expert) get a
-// zero output row.
+// zero output row. Up to kRouteLdsList pairs, the scatter goes to LDS and the
+// lists are written out contiguously at the end (scattered 4-byte stores
+// from one CU were most of this kernel's time).
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __restrict__ ids, int32_t n_pairs,
                                                               int32_t n_expert, int32_t* __restrict__ offsets,
                                                               int32_t* __restrict__ list, void* __restrict__ y,
@@ -81,6 +84,8 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
   __shared__ int32_t s_wave[kRouteThreads / 64];
   __shared__ int32_t s_bad[kRouteThreads];
   __shared__ int32_t s_nbad;
+  __shared__ int32_t s_list[kRouteLdsList];
+  const bool lds_list = n_pairs <= kRouteLdsList;  // uniform
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   constexpr int kPer = kRouteChunk / kRouteThreads;
   // Each pass over the ids takes kRouteBatch of them per thread at a time,
@@ -156,13 +161,22 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int32_t* __r
       for (int u = 0; u < kRouteBatch; ++u) {
         const int32_t p = p0 + u * kRouteThreads;
         if (p >= n_pairs) break;
-        if (id[u] >= e0 && id[u] < e0 + ne) list[atomicAdd(&s_cnt[id[u] - e0], 1)] = p;
+        if (id[u] >= e0 && id[u] < e0 + ne) {
+          const int32_t q = atomicAdd(&s_cnt[id[u] - e0], 1);
+          if (lds_list)
+            s_list[q] = p;
+          else
+            list[q] = p;
+        }
       }
     }
     base += total;
     __syncthreads();
   }
   if (tid == 0) offsets[n_expert] = base;
+  if (lds_list) {  // positions [0, base) were all written (the loop ended with a barrier)
+    for (int32_t i = tid; i < base; i += kRouteThreads) list[i] = s_list[i];
+  }
   // Pairs routed nowhere produce a zero row, cleared by the whole workgroup.
   const auto clear_row = [&](int64_t row) {
     for (int64_t col = tid; col < out_cols; col += kRouteThreads) {

@@ -82,6 +82,28 @@ def test_prefill_equals_decode_calls(cuda, qtype):
     assert rel_err(big.cpu().numpy(), _moe_ref(qtype, raws, n, k, ids, x)) <= REL_TOL_EXACT_W
 
 
+def test_prefill_route_past_lds_list(cuda):
+    """8800 pairs (1100 tokens, top-8 over 32 experts): past the 8192 whose
+    lists the routing kernel builds in LDS, so the lists are scattered
+    straight to memory. Equal bit for bit to the same tokens in decode-sized
+    calls of 100 (routed inside the kernel), and to the oracle within the
+    bars; ids routed nowhere give zero rows."""
+    n_expert, n, k, n_tokens, top_k = 32, 64, 256, 1100, 8
+    rng = np.random.default_rng(69)
+    ids = np.stack([rng.choice(n_expert, top_k, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    ids[::37, 3] = -2
+    w, per, raws, ids, x = _moe_inputs(cuda, O.Q4_0, n_expert, n, k, n_tokens, top_k, 1, 70, ids)
+    xd, idd = dev_bf16(x, cuda), torch.from_numpy(ids).to(cuda)
+    big = ops.mul_mat_id(O.Q4_0, w, per, n_expert, n, k, xd, idd, out_dtype=torch.float32)
+    parts = [ops.mul_mat_id(O.Q4_0, w, per, n_expert, n, k, xd[t:t + 100].contiguous(), idd[t:t + 100].contiguous(),
+                            out_dtype=torch.float32) for t in range(0, n_tokens, 100)]
+    torch.cuda.synchronize()
+    assert torch.equal(big, torch.cat(parts))
+    y = big.cpu().numpy()
+    assert not y[ids < 0].any()
+    check_moe(y, _moe_ref(O.Q4_0, raws, n, k, ids, x), True)
+
+
 @pytest.mark.parametrize("qtype,n_tokens", [(O.Q4_0, 150), (O.Q4_K, 150), (O.Q4_0, 600)])
 def test_prefill_glu(cuda, qtype, n_tokens):
     """The fused GLU form at 37 pairs an expert (passes of 32 over two pass
