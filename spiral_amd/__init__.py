@@ -1,7 +1,7 @@
 """spiral_amd: MI355X (gfx950) quantized-weight hot path of spiral.
 
 GGUF Q4_0 / Q8_0 / Q4_K / Q5_K / Q6_K / IQ4_NL / IQ4_XS exact dequantization to bf16 and the dequant-fused
-GEMV / GEMM / MoE grouped GEMM behind a ggml-style MUL_MAT / GET_ROWS /
+GEMV / GEMM / MoE expert products behind a ggml-style MUL_MAT / GET_ROWS /
 MUL_MAT_ID surface, as hand-written HIP kernels in libspiral_quants.so.
 
     spiral_amd._lib     ctypes binding of the C ABI (include/spiral_quants.h)
