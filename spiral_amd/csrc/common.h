@@ -161,6 +161,18 @@ __device__ __forceinline__ float iq4xs_scale(uint2 m, int b) {
   return fp16_ieee(m.x & 0xffffu) * static_cast<float>(static_cast<int>(ls) - 32);
 }
 
+// (w & mask) | hi in one v_and_or_b32, with the mask in an SGPR and hi in a
+// VGPR: a gfx9 VOP3 reads at most one scalar operand and no literal, so
+// written as C the compiler emits a v_and and a v_or with literals instead.
+// Q4_0 nibbles become fp16 pairs this way: (w & 0x000F000F) | 0x64006400 is
+// (1024 + c0, 1024 + c2) for the low nibbles of bytes 0 and 2, and the mask
+// 0x00F000F0 under 0x54005400 gives their high nibbles as (64 + c).
+__device__ __forceinline__ uint32_t and_or_b32(uint32_t w, uint32_t mask, uint32_t hi) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(hi));
+  return r;
+}
+
 // Two floats -> packed bf16 pair (lo in bits 0..15), round to nearest even.
 // Lowers to v_cvt_pk_bf16_f32 on gfx950.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {

@@ -60,13 +60,8 @@ struct MoePiece<SPIRAL_TYPE_Q4_0> {
     d = *reinterpret_cast<const uint16_t*>(we + tot * 16 + blk * 2);
   }
   __device__ __forceinline__ void zero() { q = make_uint4(0u, 0u, 0u, 0u); d = 0u; }
-  // v_and_or_b32 with the mask in an SGPR and the high bytes in a VGPR (a
-  // gfx9 VOP3 reads one scalar operand and no literal; written out, the
-  // compiler would emit a v_and and a v_or with literals instead).
   static __device__ __forceinline__ f16x2_t and_or(uint32_t w, uint32_t mask, uint32_t hi) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(mask), "v"(hi));
-    return __builtin_bit_cast(f16x2_t, r);
+    return __builtin_bit_cast(f16x2_t, and_or_b32(w, mask, hi));
   }
   __device__ __forceinline__ uint4 dequant(int s) const {
     const uint32_t w = s == 0 ? q.x : s == 1 ? q.y : s == 2 ? q.z : q.w;
