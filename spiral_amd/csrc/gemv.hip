@@ -15,6 +15,7 @@
 //      Q8_0: half a block (16 B qs + d)                            = 16 weights
 //      Q6_K: a quarter super-block (2x16 B ql, 16 B qh, 4 sub-scales, d)
 //                                                                  = 64 weights
+//            (exact form: an eighth, 2x8 B ql and 8 B qh         = 32 weights)
 //    A "unit" is J tasks per lane: tasks 64 J p + 64 j + lane of a row (pass
 //    p). Each payload load instruction of a wave reads 1 KiB of contiguous
 //    bytes. When one pass covers the row (T <= 64 J), every lane's x slice is
@@ -370,8 +371,7 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
     for (int i = 0; i < 8; ++i) x.x[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
     x.sum = reinterpret_cast<const float4*>(lds + pad64(T) * kE * 16)[u];
   }
-  // Item = (task, group): 16 x (2 x 16 B) and (SUMS) their sum.
-  template <bool SUMS = true>
+  // Item = (task, group): 16 x (2 x 16 B) and their sum.
   static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
     const int T = static_cast<int>(k / 64);
     float* xs = reinterpret_cast<float*>(lds + pad64(T) * kE * 16);
@@ -399,12 +399,11 @@ struct Fmt<SPIRAL_TYPE_Q6_K> {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const uint4 q = v[u][i];
-          if constexpr (SUMS)
-            s += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
-                 (bf16_lo(q.w) + bf16_hi(q.w));
+          s += (bf16_lo(q.x) + bf16_hi(q.x)) + (bf16_lo(q.y) + bf16_hi(q.y)) + (bf16_lo(q.z) + bf16_hi(q.z)) +
+               (bf16_lo(q.w) + bf16_hi(q.w));
           *reinterpret_cast<uint4*>(dst + 1024 * i) = q;
         }
-        if constexpr (SUMS) xs[e] = s;
+        xs[e] = s;
       }
     }
   }
@@ -832,18 +831,45 @@ struct Exact<SPIRAL_TYPE_Q8_0> : Fmt<SPIRAL_TYPE_Q8_0> {
 // ds = d * sc, (1024 + q) ds - 1056 ds = (q - 32) ds. ds has at most 18
 // significant bits (an 11-bit significand times |sc| <= 127, or 128 = 2^7),
 // so 1056 ds = 33 * 32 ds has at most 24 and is exact.
+//
+// The exact form takes 32-element tasks (the relaxed form's are 64): task t
+// of a row covers l0 .. l0 + 7 (l0 = 8 (t % 4)) of half (t / 4) % 2 of
+// super-block t / 8, in all four of the half's 16-element groups. A
+// 14336-wide row is then 448 tasks, seven full passes of a wave; 64-element
+// tasks end such a row in a half-masked fourth pass, which costs as much VALU
+// as a full one (4096 x 14336: 14.0 us against 15.5). Each lane loads 8 bytes
+// of ql twice, of qh and of the sub-scales per task.
 template <>
-struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
+struct Exact<SPIRAL_TYPE_Q6_K> {
+  static constexpr int kTaskElems = 32, kE = 4;
   static constexpr bool kRule = true;
-  // The relaxed form's staging without the group sums: the exact products
-  // take the -32 offset inside each weight.
-  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
-    Fmt<SPIRAL_TYPE_Q6_K>::stage<false>(x, k, lds);
-  }
-  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int, int u) {
-    const uint8_t* e = lds + lds_task(u, kE);
+  static __host__ __device__ int64_t lds_bytes(int64_t k) { return pad64(k / 32) * kE * 16; }
+  struct X {
+    uint4 x[4];  // group j's 8 x values
+  };
+  static __device__ __forceinline__ void xload(X& x, const uint8_t* lds, int, int t) {
+    const uint8_t* e = lds + lds_task(t, kE);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x.x[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+    for (int i = 0; i < 4; ++i) x.x[i] = *reinterpret_cast<const uint4*>(e + 1024 * i);
+  }
+  // Item = (task, group): x[256 (t / 8) + 128 ((t / 4) % 2) + 32 j + 8 (t % 4)], 8 values.
+  static __device__ void stage(const uint16_t* __restrict__ x, int64_t k, uint8_t* lds) {
+    const int T = static_cast<int>(k / 32);
+    const int items = 4 * T;
+    for (int e0 = threadIdx.x; e0 < items; e0 += kStageUnroll * blockDim.x) {
+      uint4 v[kStageUnroll];
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int e = min(e0 + u * static_cast<int>(blockDim.x), items - 1);
+        const int t = e >> 2, j = e & 3;
+        v[u] = *reinterpret_cast<const uint4*>(x + (t >> 3) * 256 + ((t >> 2) & 1) * 128 + 32 * j + 8 * (t & 3));
+      }
+#pragma unroll
+      for (int u = 0; u < kStageUnroll; ++u) {
+        const int e = e0 + u * static_cast<int>(blockDim.x);
+        if (e < items) *reinterpret_cast<uint4*>(lds + lds_task(e >> 2, kE) + 1024 * (e & 3)) = v[u];
+      }
+    }
   }
   struct Planes {
     __amdgpu_buffer_rsrc_t ql, qh, sc, d;
@@ -858,28 +884,32 @@ struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
                   static_cast<uint32_t>(nb)};
   }
   struct Payload {
-    uint4 a, b, h;
-    uint2 sc8;      // the 8 sub-scales of the task's half super-block
-    uint32_t odd;   // 16-lane half: its groups' sub-scales are the odd bytes
+    uint2 a, b, h;
+    uint2 sc8;     // the 8 sub-scales of the task's half super-block
+    uint32_t odd;  // l0 >= 16: its groups' sub-scales are the odd bytes
     _Float16 d;
   };
-  // Task u: super-block u / 4, half (u >> 1) & 1, 16-lane half u & 1 (as
-  // load()). Loaded values are only stored here: arithmetic on them would
-  // make the compiler wait for the load at once.
+  static __device__ __forceinline__ uint2 bload8nt(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    const auto x = __builtin_amdgcn_raw_buffer_load_b64(r, v, s, kStreamAux);
+    return make_uint2(x[0], x[1]);
+  }
+  // Lane = task tb + lane: super-block tb / 8 + lane / 8, half (lane / 4) % 2,
+  // l0 = 8 (lane % 4). Loaded values are only stored here: arithmetic on them
+  // would make the compiler wait for the load at once.
   static __device__ __forceinline__ void bload(Payload& p, const Planes& P, bool none, uint32_t rr, uint32_t tb,
                                                uint32_t lane, uint32_t lsk) {
-    const uint32_t sb = rr * P.nb + (tb >> 2), ls = lane >> 2, hh = (lane >> 1) & 1u, s = lane & 1u;
-    const uint32_t lo = ls * 128u + 64u * hh + 16u * s;
+    const uint32_t sb = rr * P.nb + (tb >> 3), ls = lane >> 3, hh = (lane >> 2) & 1u, q4 = lane & 3u;
+    const uint32_t lo = ls * 128u + 64u * hh + 8u * q4;
     const __amdgpu_buffer_rsrc_t ql = rsrc_or_none(P.ql, none);
-    p.a = bload16(ql, lo | lsk, sb * 128u);
-    p.b = bload16(ql, (lo + 32u) | lsk, sb * 128u);
-    p.h = bload16(rsrc_or_none(P.qh, none), (ls * 64u + 32u * hh + 16u * s) | lsk, sb * 64u);
+    p.a = bload8nt(ql, lo | lsk, sb * 128u);
+    p.b = bload8nt(ql, (lo + 32u) | lsk, sb * 128u);
+    p.h = bload8nt(rsrc_or_none(P.qh, none), (ls * 64u + 32u * hh + 8u * q4) | lsk, sb * 64u);
     p.sc8 = bload8(rsrc_or_none(P.sc, none), (ls * 16u + 8u * hh) | lsk, sb * 16u);
-    p.odd = s;
+    p.odd = q4 >> 1;
     p.d = bload_h(rsrc_or_none(P.d, none), (ls * 2u) | lsk, sb * 2u);
   }
-  // Sub-scale of group j is sc[8 h + s + 2 j]: bytes s, s + 2, s + 4, s + 6
-  // of the half's 8 sub-scales.
+  // Sub-scale of group j is sc[8 h + l0 / 16 + 2 j]: bytes s, s + 2, s + 4,
+  // s + 6 of the half's 8 sub-scales (s = odd).
   static __device__ __forceinline__ uint32_t sub_scales(const Payload& p) {
     return __builtin_amdgcn_perm(p.sc8.y, p.sc8.x, p.odd ? 0x07050301u : 0x06040200u);
   }
@@ -902,11 +932,10 @@ struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
     return terms(fp16_scale(fp16_bits(p.d)), sub_scales(p));
   }
   static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
-    const uint32_t A[4] = {p.a.x, p.a.y, p.a.z, p.a.w}, B[4] = {p.b.x, p.b.y, p.b.z, p.b.w};
-    const uint32_t H[4] = {p.h.x, p.h.y, p.h.z, p.h.w};
+    const uint32_t A[2] = {p.a.x, p.a.y}, B[2] = {p.b.x, p.b.y}, H[2] = {p.h.x, p.h.y};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // 6-bit codes of elements 4q .. 4q+3 of each group, one per byte.
+    for (int q = 0; q < 2; ++q) {
+      // 6-bit codes of elements l0 + 4q .. l0 + 4q + 3 of each group, one per byte.
       const uint32_t c[4] = {
           (A[q] & 0x0F0F0F0Fu) | ((H[q] << 4) & 0x30303030u),
           (B[q] & 0x0F0F0F0Fu) | ((H[q] << 2) & 0x30303030u),
@@ -915,9 +944,9 @@ struct Exact<SPIRAL_TYPE_Q6_K> : Fmt<SPIRAL_TYPE_Q6_K> {
       };
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint4 xv = x.x[2 * j + (q >> 1)];
-        a0 = dot2(wpair<kHi1024, kSel01>(c[j], s.ds[j], s.c[j]), (q & 1) ? xv.z : xv.x, a0);
-        a1 = dot2(wpair<kHi1024, kSel23>(c[j], s.ds[j], s.c[j]), (q & 1) ? xv.w : xv.y, a1);
+        const uint4 xv = x.x[j];
+        a0 = dot2(wpair<kHi1024, kSel01>(c[j], s.ds[j], s.c[j]), q ? xv.z : xv.x, a0);
+        a1 = dot2(wpair<kHi1024, kSel23>(c[j], s.ds[j], s.c[j]), q ? xv.w : xv.y, a1);
       }
     }
   }
