@@ -1435,6 +1435,12 @@ int launch_exact(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, vo
   if (TYPE == SPIRAL_TYPE_Q6_K) return launch_exact_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
   if (T <= 64) return launch_exact_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
   if (T <= 128) return launch_exact_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  // Longer rows: the widest unit whose passes tile the row exactly. A
+  // partly masked last pass costs the VALU of a full one (4096 x 14336 Q4_0
+  // is 448 tasks: seven passes of 64 instead of two of 256, the second a
+  // quarter empty).
+  if (T % 256 != 0 && T % 128 == 0) return launch_exact_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if (T % 256 != 0 && T % 64 == 0) return launch_exact_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
   return launch_exact_j<F, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
 }
 
