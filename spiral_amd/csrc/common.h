@@ -214,19 +214,25 @@ __device__ __forceinline__ float dpp_f32(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
 }
 
-// Sum over the wave's 64 lanes in six DPP adds (no LDS round trips): pairs,
-// quads, then the four quads of each 16-lane row (rotations by 4 and 8), then
-// the rows (broadcasts of lane 15 and lane 31). The total is exact in lane 63
-// only; other lanes hold partial sums.
-__device__ __forceinline__ float wave_sum_last(float v) {
+// Sum over each group of G consecutive lanes (G = 16, 32 or 64) in DPP adds
+// (no LDS round trips): pairs, quads, then the four quads of each 16-lane row
+// (rotations by 4 and 8, after which every lane of a row holds the row's
+// sum), then the rows (broadcasts of lane 15 and lane 31). A group's sum is
+// exact in its last lane; other lanes may hold partial sums.
+template <int G>
+__device__ __forceinline__ float group_sum_last(float v) {
+  static_assert(G == 16 || G == 32 || G == 64, "groups of 16, 32 or 64 lanes");
   v += dpp_f32<0xB1, 0xF>(v);   // quad_perm [1, 0, 3, 2]
   v += dpp_f32<0x4E, 0xF>(v);   // quad_perm [2, 3, 0, 1]
   v += dpp_f32<0x124, 0xF>(v);  // row_ror 4
   v += dpp_f32<0x128, 0xF>(v);  // row_ror 8
-  v += dpp_f32<0x142, 0xA>(v);  // row_bcast 15: row 0 into row 1, row 2 into row 3
-  v += dpp_f32<0x143, 0xC>(v);  // row_bcast 31: rows 0-1 into rows 2 and 3
+  if constexpr (G >= 32) v += dpp_f32<0x142, 0xA>(v);  // row_bcast 15: row 0 into row 1, row 2 into row 3
+  if constexpr (G == 64) v += dpp_f32<0x143, 0xC>(v);  // row_bcast 31: rows 0-1 into rows 2 and 3
   return v;
 }
+
+// Sum over the wave's 64 lanes, exact in lane 63.
+__device__ __forceinline__ float wave_sum_last(float v) { return group_sum_last<64>(v); }
 
 // ---- host-side helpers ----------------------------------------------------------
 

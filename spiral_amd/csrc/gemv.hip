@@ -1227,46 +1227,62 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_kernel(const uint8_t* _
 // per-lane part, fixed for the wave, and the row and pass, in a scalar
 // register, so a refill costs no vector instructions.
 
-template <class F, int J, bool MASK>
+// A unit is one pass over RG = 64 / G rows: lane group g = lane / G takes
+// row rr + g, tasks tb + lane % G. A format addresses task tb + lane of row
+// rr over planes that hold rows of T tasks back to back, so the group's row
+// enters as the lane index g T + lane % G (tb and T are multiples of 8, which
+// keeps a super-block's eight tasks within one lane index range). Lanes of a
+// row past the wave's last (row_end rows from rr) or of a task past the row's
+// end are skipped.
+template <class F, int J, int G, bool MASK>
 __device__ __forceinline__ void bload_unit(Unit<F, J>& U, const typename F::Planes& P, bool none, int rr, int pass,
-                                           int T, int lane) {
+                                           int T, int lane, int row_end) {
+  const int gl = lane % G;
+  const uint32_t vl = static_cast<uint32_t>((lane / G) * T + gl);
+  const bool row_out = G < 64 && lane / G >= row_end;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int tb = pass * 64 * J + 64 * j;
-    const uint32_t lsk = (MASK && tb + lane >= T) ? kSkip : 0u;
-    F::bload(U.p[j], P, none, static_cast<uint32_t>(rr), static_cast<uint32_t>(tb), static_cast<uint32_t>(lane), lsk);
+    const int tb = pass * G * J + G * j;
+    const uint32_t lsk = ((MASK && tb + gl >= T) || row_out) ? kSkip : 0u;
+    F::bload(U.p[j], P, none, static_cast<uint32_t>(rr), static_cast<uint32_t>(tb), vl, lsk);
   }
 }
 
-template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT, int MINW>
+template <class F, int J, int G, int WAVES, int DEPTH, bool XREG, bool MASK, bool F32_OUT, int MINW>
 __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint8_t* __restrict__ w, int64_t n_rows,
                                                                       int64_t k, const uint16_t* __restrict__ x,
                                                                       void* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int kEsize = F32_OUT ? 4 : 2;
+  constexpr int RG = 64 / G;  // rows per unit
   const int lane = threadIdx.x & 63;
+  const int gl = lane % G, grp = lane / G;
   const int64_t wave =
       static_cast<int64_t>(blockIdx.x) * WAVES + __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t n_waves = static_cast<int64_t>(gridDim.x) * WAVES;
-  const int64_t r0 = wave * n_rows / n_waves, r1 = (wave + 1) * n_rows / n_waves;
+  // Waves take whole groups of RG rows; only the matrix's last group can be short.
+  const int64_t n_groups = (n_rows + RG - 1) / RG;
+  const int64_t g0 = wave * n_groups / n_waves * RG, g1 = (wave + 1) * n_groups / n_waves * RG;
+  const int64_t r0 = g0 < n_rows ? g0 : n_rows, r1 = g1 < n_rows ? g1 : n_rows;
+  const int rows = static_cast<int>(r1 - r0);
   const int T = static_cast<int>(k / F::kTaskElems);
-  const int passes = XREG ? 1 : (T + 64 * J - 1) / (64 * J);
-  const int units = static_cast<int>(r1 - r0) * passes;
+  const int passes = XREG ? 1 : (T + G * J - 1) / (G * J);
+  const int units = (rows + RG - 1) / RG * passes;
   const typename F::Planes P = F::planes(w, n_rows, k, r0, r1);
   const __amdgpu_buffer_rsrc_t Y = rsrc(static_cast<uint8_t*>(y) + r0 * kEsize, (r1 - r0) * kEsize);
 
-  // Unit coordinates (row relative to r0, pass) advance one pass at a time:
-  // (rl, pl) for loads, (rc, pc) for compute.
+  // Unit coordinates (first row relative to r0, pass) advance one pass at a
+  // time: (rl, pl) for loads, (rc, pc) for compute.
   Unit<F, J> buf[DEPTH];
   int rl = 0, pl = 0;
   auto advance = [&](int& r, int& pass) {
-    if (++pass == passes) { pass = 0; ++r; }
+    if (++pass == passes) { pass = 0; r += RG; }
   };
   // Issued slot by slot in the loop's order, so that the loop header sees
   // the same sequence of loads in flight from the prologue as from the loop.
 #pragma unroll
   for (int d = 0; d < DEPTH; ++d) {
-    bload_unit<F, J, MASK>(buf[d], P, d >= units, rl, pl, T, lane);
+    bload_unit<F, J, G, MASK>(buf[d], P, d >= units, rl, pl, T, lane, rows - rl);
     advance(rl, pl);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -1277,7 +1293,7 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint
   if constexpr (XREG) {
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const int t = 64 * j + lane;
+      const int t = G * j + gl;
       F::xload(xr[j], lds, T, t < T ? t : 0);
     }
   }
@@ -1303,7 +1319,7 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint
       if constexpr (XREG) {
         F::dot(U.p[j], xr[j], sc[j], a0, a1);
       } else {
-        const int t = pc * 64 * J + 64 * j + lane;
+        const int t = pc * G * J + G * j + gl;
         typename F::X xt;
         F::xload(xt, lds, T, t < T ? t : 0);
         F::dot(U.p[j], xt, sc[j], a0, a1);
@@ -1312,10 +1328,11 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint
     const bool end = XREG || pc == passes - 1;
     float v = 0.0f;
     if (end) {
-      v = wave_sum_last(a0 + a1);
+      v = group_sum_last<G>(a0 + a1);
       a0 = a1 = 0.0f;
     }
-    const uint32_t off = static_cast<uint32_t>(rc * kEsize) | ((lane == 63 && end) ? 0u : kSkip);
+    const bool store = end && gl == G - 1 && (G == 64 || grp < rows - rc);
+    const uint32_t off = static_cast<uint32_t>((rc + grp) * kEsize) | (store ? 0u : kSkip);
     if constexpr (F32_OUT)
       __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), Y, off, 0, 0);
     else
@@ -1332,7 +1349,7 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint
     for (int d = 0; d < DEPTH; ++d) {
       compute(buf[d]);
       __builtin_amdgcn_sched_barrier(0);
-      bload_unit<F, J, MASK>(buf[d], P, u + d + DEPTH >= units, rl, pl, T, lane);
+      bload_unit<F, J, G, MASK>(buf[d], P, u + d + DEPTH >= units, rl, pl, T, lane, rows - rl);
       advance(rl, pl);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1342,36 +1359,43 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint
     if (u + d < units) compute(buf[d]);
 }
 
-template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, int MINW>
+template <class F, int J, int G, int WAVES, int DEPTH, bool XREG, bool MASK, int MINW>
 int launch_exact_cfg(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
+  constexpr int RG = 64 / G;
   const int64_t lds = F::lds_bytes(k);
-  const void* kern = y_type == SPIRAL_TYPE_F32
-                         ? reinterpret_cast<const void*>(gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, true, MINW>)
-                         : reinterpret_cast<const void*>(gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, false, MINW>);
+  const void* kern =
+      y_type == SPIRAL_TYPE_F32
+          ? reinterpret_cast<const void*>(gemv_exact_kernel<F, J, G, WAVES, DEPTH, XREG, MASK, true, MINW>)
+          : reinterpret_cast<const void*>(gemv_exact_kernel<F, J, G, WAVES, DEPTH, XREG, MASK, false, MINW>);
   const int64_t resident = static_cast<int64_t>(device_cu_count()) * blocks_per_cu(kern, 64 * WAVES, lds);
-  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n_rows, WAVES), resident));
+  const int64_t n_groups = ceil_div(n_rows, RG);
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(n_groups, WAVES), resident));
   // A wave's rows of a plane (at most one byte per element) must stay below
   // 2 GiB: bit 31 of an offset marks a skipped access.
-  if (ceil_div(n_rows, blocks * WAVES) * k >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
+  if (ceil_div(n_groups, blocks * WAVES) * RG * k >= (int64_t(1) << 31)) return SPIRAL_ERR_SHAPE;
   const uint8_t* W = static_cast<const uint8_t*>(w);
   if (y_type == SPIRAL_TYPE_F32)
-    hipLaunchKernelGGL((gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, true, MINW>),
+    hipLaunchKernelGGL((gemv_exact_kernel<F, J, G, WAVES, DEPTH, XREG, MASK, true, MINW>),
                        dim3(static_cast<unsigned>(blocks)), dim3(64 * WAVES), lds, s, W, n_rows, k, x, y);
   else
-    hipLaunchKernelGGL((gemv_exact_kernel<F, J, WAVES, DEPTH, XREG, MASK, false, MINW>),
+    hipLaunchKernelGGL((gemv_exact_kernel<F, J, G, WAVES, DEPTH, XREG, MASK, false, MINW>),
                        dim3(static_cast<unsigned>(blocks)), dim3(64 * WAVES), lds, s, W, n_rows, k, x, y);
   return launch_status();
 }
 
-template <class F, int J, int WAVES, int DEPTH, int MINW = 1>
+// Units of G lanes a row and J tasks a lane. Narrow groups (G < 64) serve
+// rows longer than one unit, so they keep x in LDS.
+template <class F, int J, int G, int WAVES, int DEPTH, int MINW = 1>
 int launch_exact_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   const int64_t T = k / F::kTaskElems;
-  const bool mask = T % (64 * J) != 0;
-  if (T <= 64 * J)
-    return mask ? launch_exact_cfg<F, J, WAVES, DEPTH, true, true, MINW>(w, n_rows, k, x, y, y_type, s)
-                : launch_exact_cfg<F, J, WAVES, DEPTH, true, false, MINW>(w, n_rows, k, x, y, y_type, s);
-  return mask ? launch_exact_cfg<F, J, WAVES, DEPTH, false, true, MINW>(w, n_rows, k, x, y, y_type, s)
-              : launch_exact_cfg<F, J, WAVES, DEPTH, false, false, MINW>(w, n_rows, k, x, y, y_type, s);
+  const bool mask = T % (G * J) != 0;
+  if constexpr (G == 64) {
+    if (T <= 64 * J)
+      return mask ? launch_exact_cfg<F, J, G, WAVES, DEPTH, true, true, MINW>(w, n_rows, k, x, y, y_type, s)
+                  : launch_exact_cfg<F, J, G, WAVES, DEPTH, true, false, MINW>(w, n_rows, k, x, y, y_type, s);
+  }
+  return mask ? launch_exact_cfg<F, J, G, WAVES, DEPTH, false, true, MINW>(w, n_rows, k, x, y, y_type, s)
+              : launch_exact_cfg<F, J, G, WAVES, DEPTH, false, false, MINW>(w, n_rows, k, x, y, y_type, s);
 }
 
 template <class F, int J, int WAVES, int DEPTH, bool XREG, bool MASK, int MINW = 1>
@@ -1421,27 +1445,66 @@ template <int TYPE>
 int launch_relaxed(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   using F = Fmt<TYPE>;
   const int64_t T = k / F::kTaskElems;
-  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 64) return launch_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 128) return launch_j<F, 2, TYPE == SPIRAL_TYPE_Q5_K ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
-  return launch_j<F, 4, TYPE == SPIRAL_TYPE_Q8_0 ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
+  if constexpr (TYPE == SPIRAL_TYPE_Q6_K) {
+    return launch_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
+  } else {
+    if (T <= 64) return launch_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
+    if (T <= 128) return launch_j<F, 2, TYPE == SPIRAL_TYPE_Q5_K ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
+    return launch_j<F, 4, TYPE == SPIRAL_TYPE_Q8_0 ? 12 : 8, 2>(w, n_rows, k, x, y, y_type, s);
+  }
 }
 
-// Exact mode: the same unit shapes.
+// Exact mode: the unit shape of least estimated work, the wider on a tie.
+// Whole-wave units (G = 64) give a row U = 64 J task slots a pass; rows of up
+// to 256 tasks can instead take 16 or 32 lanes a row, four or two
+// neighbouring rows a unit. The estimate counts each row's passes times J
+// tasks a lane: a partly masked last pass costs the VALU of a full one. A
+// task costs 32 (x read from LDS), 28 with x in registers (one pass) and 35
+// in narrow groups, factors fitted to these MI355X timings (us):
+//                          64 lanes, LDS    64 lanes, regs   narrow groups
+//   262144 x 1536 Q6_K                        79.3 (J 1)      72.9 (16 x 3)
+//   13824 x 5120 Q4_K       17.4 (3 passes)   19.2 (J 4)      15.9 (32 x 5)
+//   27648 x 5120 Q6_K       33.6 (3 passes)                   29.8 (32 x 5)
+//   14336 x 5120 IQ4_XS     19.2 (3 passes)   21.8 (J 4)      17.1 (32 x 5)
+//   18944 x 3584 Q4_0                         12.4 (J 2)      13.8 (16 x 7)
+// Longer rows keep whole-wave units: a unit of narrow groups reads distant
+// rows in small pieces (5120 x 13824 Q6_K: 36.7 us in 16-lane groups against
+// 21.3 in passes of 64).
+inline int64_t exact_work(int64_t T, int G, int J) {
+  const bool xreg = G == 64 && T <= 64 * J;
+  const int64_t passes = xreg ? 1 : ceil_div(T, G * J);
+  return passes * J * (G < 64 ? 35 : xreg ? 28 : 32) * G;  // per 64 rows
+}
+
+inline int exact_unit(int64_t T, int max_u) {
+  struct Shape {
+    int u, g, j;
+  };
+  constexpr Shape kShapes[] = {{256, 64, 4}, {128, 64, 2}, {64, 64, 1}, {32, 32, 1}, {16, 16, 1}};
+  int best = 0;
+  int64_t best_work = 0;
+  for (const Shape& c : kShapes) {
+    if (c.u > max_u || (c.g < 64 && T > 256)) continue;
+    const int64_t work = exact_work(T, c.g, c.j);
+    if (best == 0 || work < best_work) best = c.u, best_work = work;
+  }
+  return best;
+}
+
 template <int TYPE>
 int launch_exact(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   using F = Exact<TYPE>;
-  const int64_t T = k / F::kTaskElems;
-  if (TYPE == SPIRAL_TYPE_Q6_K) return launch_exact_j<F, 1, 16, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 64) return launch_exact_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T <= 128) return launch_exact_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  // Longer rows: the widest unit whose passes tile the row exactly. A
-  // partly masked last pass costs the VALU of a full one (4096 x 14336 Q4_0
-  // is 448 tasks: seven passes of 64 instead of two of 256, the second a
-  // quarter empty).
-  if (T % 256 != 0 && T % 128 == 0) return launch_exact_j<F, 2, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  if (T % 256 != 0 && T % 64 == 0) return launch_exact_j<F, 1, 8, 2>(w, n_rows, k, x, y, y_type, s);
-  return launch_exact_j<F, 4, 8, 2>(w, n_rows, k, x, y, y_type, s);
+  // Q6_K: one task a lane, 16-wave workgroups (x staged once per 16 rows).
+  constexpr bool kQ6 = TYPE == SPIRAL_TYPE_Q6_K;
+  constexpr int WAVES = kQ6 ? 16 : 8;
+  const int u = exact_unit(k / F::kTaskElems, kQ6 ? 64 : 256);
+  if (u == 16) return launch_exact_j<F, 1, 16, WAVES, 2>(w, n_rows, k, x, y, y_type, s);
+  if (u == 32) return launch_exact_j<F, 1, 32, WAVES, 2>(w, n_rows, k, x, y, y_type, s);
+  if constexpr (!kQ6) {
+    if (u == 128) return launch_exact_j<F, 2, 64, WAVES, 2>(w, n_rows, k, x, y, y_type, s);
+    if (u == 256) return launch_exact_j<F, 4, 64, WAVES, 2>(w, n_rows, k, x, y, y_type, s);
+  }
+  return launch_exact_j<F, 1, 64, WAVES, 2>(w, n_rows, k, x, y, y_type, s);
 }
 
 template <int TYPE>

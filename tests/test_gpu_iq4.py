@@ -109,10 +109,11 @@ def test_get_rows(cuda, qtype):
 
 @pytest.mark.parametrize("qtype,n,k", [(O.IQ4_NL, 1, 32), (O.IQ4_NL, 7, 32 * 17), (O.IQ4_NL, 129, 4096),
                                        (O.IQ4_NL, 70, 14336), (O.IQ4_XS, 5, 256), (O.IQ4_XS, 129, 4096),
-                                       (O.IQ4_XS, 70, 14336), (O.IQ4_XS, 33, 256 * 9)])
+                                       (O.IQ4_XS, 70, 14336), (O.IQ4_XS, 33, 256 * 9), (O.IQ4_NL, 46, 32 * 96),
+                                       (O.IQ4_XS, 45, 256 * 20)])
 def test_gemv(cuda, qtype, n, k):
-    """One task per lane, x in registers, several passes with x from LDS,
-    masked tasks."""
+    """Rows in 16- and 32-lane groups (masked tasks at 32 * 17 and 256 * 9),
+    x in registers, several passes with x from LDS."""
     raw = iq4_weights(qtype, n, k, 20 + n, specials=False)
     for out_dtype in (torch.bfloat16, torch.float32):
         y, x = _mul_mat(cuda, qtype, raw, n, k, 1, 21 + n, out_dtype)

@@ -169,10 +169,11 @@ def _mul_mat(cuda, qtype, raw, n, k, m, seed, out_dtype):
 
 
 @pytest.mark.parametrize("qtype", KQ)
-@pytest.mark.parametrize("n,k", [(1, 256), (7, 512), (129, 4096), (70, 14336), (33, 256 * 9)])
+@pytest.mark.parametrize("n,k", [(1, 256), (7, 512), (129, 4096), (70, 14336), (33, 256 * 9), (45, 256 * 20)])
 def test_gemv(cuda, qtype, n, k):
-    """One task per lane (k <= 2048), two (4096, x in registers), several
-    passes with x from LDS (14336), a pass with masked tasks (2304)."""
+    """Rows in 16-lane groups, four a unit (256, 512, and 2304 with masked
+    tasks), two tasks a lane with x in registers (4096), several passes with
+    x from LDS (14336), 32-lane groups over five passes (5120)."""
     raw = kq_weights(qtype, n, k, 20 + n, specials=False)
     for out_dtype in (torch.bfloat16, torch.float32):
         y, x = _mul_mat(cuda, qtype, raw, n, k, 1, 21 + n, out_dtype)

@@ -170,8 +170,9 @@ def test_gemv_small(cuda, qtype, out_dtype):
 
 @pytest.mark.parametrize("k_blocks", [17, 65, 127, 129, 192, 257])
 def test_gemv_q8_0_scale_spans(cuda, k_blocks):
-    """Rows with an odd number of blocks, one pass with x in registers (17:
-    one task per lane, 65 and 127: four) or several passes from LDS (129 and
+    """Rows with an odd number of blocks (two tasks a block): 16-lane groups
+    with masked tasks (17, 65), one pass of four tasks a lane with x in
+    registers (127), or several passes of whole-wave units from LDS (129 and
     257, a masked last pass; 192: even)."""
     k = 32 * k_blocks
     y, ref = _mul_mat_case(cuda, O.Q8_0, 37, k, 1, 40 + k_blocks, torch.float32)

@@ -117,8 +117,9 @@ def run_mul_mat(cuda, qtype, n, k, m, seed, out_dtype):
     return y.float().cpu().numpy(), O.dequant(qtype, raw, n, k), x
 
 
-# k: one pass with x in registers, and several passes with x read from LDS
-GEMV_K = {O.Q4_0: (32 * 12, 32 * 288), O.Q8_0: (32 * 12, 32 * 160), O.Q6_K: (256 * 3, 256 * 24)}
+# k: rows in 16- or 32-lane groups, and several passes of whole-wave units
+# with x read from LDS
+GEMV_K = {O.Q4_0: (32 * 12, 32 * 288), O.Q8_0: (32 * 12, 32 * 160), O.Q6_K: (256 * 3, 256 * 6, 256 * 24)}
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
