@@ -1319,9 +1319,11 @@ __global__ void __launch_bounds__(64 * WAVES, MINW) gemv_exact_kernel(const uint
       if constexpr (XREG) {
         F::dot(U.p[j], xr[j], sc[j], a0, a1);
       } else {
-        const int t = pc * G * J + G * j + gl;
+        // Whole-wave units with no masked task read x at a wave-uniform
+        // 64-task block plus the lane's slot.
+        const int t = (G == 64 && !MASK) ? (((pc * J + j) << 6) | lane) : pc * G * J + G * j + gl;
         typename F::X xt;
-        F::xload(xt, lds, T, t < T ? t : 0);
+        F::xload(xt, lds, T, (!MASK || t < T) ? t : 0);
         F::dot(U.p[j], xt, sc[j], a0, a1);
       }
     }
