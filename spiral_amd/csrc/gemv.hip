@@ -20,7 +20,10 @@
 //    p). Each payload load instruction of a wave reads 1 KiB of contiguous
 //    bytes. When one pass covers the row (T <= 64 J), every lane's x slice is
 //    the same for all rows and lives in registers (XREG); otherwise it is
-//    read from LDS per unit.
+//    read from LDS per unit. The exact kernel can also give a row G = 16 or
+//    32 lanes, so that a unit covers four or two neighbouring rows (rows of
+//    up to 256 tasks that are no multiple of 64); launch_exact picks the
+//    unit shape of least estimated work.
 //  - Units are software-pipelined: the payload of unit u + 1 is in flight
 //    while unit u is computed, and the first unit is requested before x is
 //    staged, so the HBM latency of the first loads overlaps the staging.
@@ -28,8 +31,9 @@
 //    sits at ((t / 64) E + e) KiB + (t % 64) 16 bytes, so a wave reading
 //    entry e of its 64 tasks touches 1 KiB of consecutive LDS and e is an
 //    immediate offset. Per-task sums of x follow the entries.
-//  - A row's fp32 partial sums are reduced across the wave after its last
-//    pass with DPP (six adds, the total in lane 63) and lane 63 stores y.
+//  - A row's fp32 partial sums are reduced across the wave (or its lane
+//    group) after its last pass with DPP (six adds for 64 lanes, the total
+//    in the last lane), and that lane stores y.
 //
 // Arithmetic (fp32 accumulation throughout). Two modes share the kernel:
 //  - Exact (the default, Exact<TYPE>): every weight is the dequantized bf16
