@@ -141,6 +141,22 @@ __device__ __forceinline__ uint32_t kq_scale_min(uint32_t s0, uint32_t s1, uint3
   return sc | (mn << 8);
 }
 
+// kq_scale_min of groups 2j and 2j + 1 (chunk j = 0..3: the low and high
+// nibbles of 32 qs bytes) as bytes (scale 2j, min 2j, scale 2j + 1, min
+// 2j + 1), with no branch on j: two v_perm_b32 gather bytes o and o + 1
+// (o = 2 (j % 2)) of s0, s1 and s2, and a bit select on j / 2 picks the
+// 6-bit fields (groups 0..3) or the nibbles of s2 under the top bits of s0
+// and s1 (groups 4..7).
+__device__ __forceinline__ uint32_t kq_chunk_scales(uint32_t s0, uint32_t s1, uint32_t s2, uint32_t j) {
+  const uint32_t sel = 0x05010400u + 2u * (j & 1u) * 0x01010101u;
+  const uint32_t a = __builtin_amdgcn_perm(s1, s0, sel);       // s0[o], s1[o], s0[o + 1], s1[o + 1]
+  const uint32_t c = __builtin_amdgcn_perm(s2 >> 4, s2, sel);  // s2[o] and its high nibble, the same for o + 1
+  const uint32_t lo = a & 0x3F3F3F3Fu;
+  const uint32_t hi = (c & 0x0F0F0F0Fu) | ((a >> 2) & 0x30303030u);
+  const uint32_t m = 0u - (j >> 1);
+  return (hi & m) | (lo & ~m);
+}
+
 // IQ4 codebook entries of four 4-bit indices held one per byte of c (values
 // 0..15), as bytes kv + 128 (1..241) of ggml's kvalues_iq4nl
 // {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113}:

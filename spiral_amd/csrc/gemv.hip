@@ -543,13 +543,12 @@ struct FmtKQ {
       b0 = dot2(bf16_01(hi), (i & 1) ? eh.z : eh.x, b0);
       b1 = dot2(bf16_23(hi), (i & 1) ? eh.w : eh.y, b1);
     }
-    const uint32_t sl = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2));
-    const uint32_t sh = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2) + 1);
+    const uint32_t sm = kq_chunk_scales(p.meta.y, p.meta.z, p.meta.w, p.c2 >> 1);
     const float d = fp16_ieee(p.meta.x & 0xffffu), dmin = fp16_ieee(p.meta.x >> 16);
     // bf16 (128 + q) against x: remove 128 * sum(x) per group.
-    const float gl = static_cast<float>(sl & 0xffu) * ((a0 + a1) - 128.0f * x.sum.x);
-    const float gh = static_cast<float>(sh & 0xffu) * ((b0 + b1) - 128.0f * x.sum.y);
-    const float ml = static_cast<float>(sl >> 8) * x.sum.x + static_cast<float>(sh >> 8) * x.sum.y;
+    const float gl = static_cast<float>(sm & 0xffu) * ((a0 + a1) - 128.0f * x.sum.x);
+    const float gh = static_cast<float>((sm >> 16) & 0xffu) * ((b0 + b1) - 128.0f * x.sum.y);
+    const float ml = static_cast<float>((sm >> 8) & 0xffu) * x.sum.x + static_cast<float>(sm >> 24) * x.sum.y;
     return d * (gl + gh) - dmin * ml;
   }
 };
@@ -1002,11 +1001,10 @@ struct ExactKQ : FmtKQ<TYPE> {
     float dl, ml, dh, mh;
   };
   static __device__ __forceinline__ S scale(const Payload& p, bool&) {
-    const uint32_t sl = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2));
-    const uint32_t sh = kq_scale_min(p.meta.y, p.meta.z, p.meta.w, static_cast<int>(p.c2) + 1);
+    const uint32_t sm = kq_chunk_scales(p.meta.y, p.meta.z, p.meta.w, p.c2 >> 1);
     const float d24 = fp16_ieee(p.meta.x & 0xffffu) * kTwo24, dmin = fp16_ieee(p.meta.x >> 16);
-    return S{d24 * static_cast<float>(sl & 0xffu), -(dmin * static_cast<float>(sl >> 8)),
-             d24 * static_cast<float>(sh & 0xffu), -(dmin * static_cast<float>(sh >> 8))};
+    return S{d24 * static_cast<float>(sm & 0xffu), -(dmin * static_cast<float>((sm >> 8) & 0xffu)),
+             d24 * static_cast<float>((sm >> 16) & 0xffu), -(dmin * static_cast<float>(sm >> 24))};
   }
   static __device__ __forceinline__ S scale_rule(const Payload& p) {
     bool unused = false;

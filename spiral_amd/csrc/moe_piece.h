@@ -186,13 +186,12 @@ struct MoePieceKQ {
     return 64 * (g >> 1) + (s < 2 ? 16 * (g & 1) + 8 * s : 32 + 16 * (g & 1) + 8 * (s - 2)) + e;
   }
   __device__ __forceinline__ void prep() {
-    const uint32_t sl = kq_scale_min(meta.y, meta.z, meta.w, grp);
-    const uint32_t sh = kq_scale_min(meta.y, meta.z, meta.w, grp + 1);
+    const uint32_t sm = kq_chunk_scales(meta.y, meta.z, meta.w, static_cast<uint32_t>(grp) >> 1);
     const float d = fp16_ieee(meta.x & 0xffffu), dm = fp16_ieee(meta.x >> 16);
-    d0 = d * static_cast<float>(sl & 0xffu);
-    m0 = -(dm * static_cast<float>(sl >> 8));
-    d1 = d * static_cast<float>(sh & 0xffu);
-    m1 = -(dm * static_cast<float>(sh >> 8));
+    d0 = d * static_cast<float>(sm & 0xffu);
+    m0 = -(dm * static_cast<float>((sm >> 8) & 0xffu));
+    d1 = d * static_cast<float>((sm >> 16) & 0xffu);
+    m1 = -(dm * static_cast<float>(sm >> 24));
   }
   __device__ __forceinline__ void zero() { q = meta = qh = make_uint4(0u, 0u, 0u, 0u); grp = 0; }
   __device__ __forceinline__ uint4 dequant(int s) const {
