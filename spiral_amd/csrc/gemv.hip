@@ -1013,12 +1013,15 @@ struct ExactKQ : FmtKQ<TYPE> {
   static __device__ __forceinline__ void dot(const Payload& p, const X& x, const S& s, float& a0, float& a1) {
     const uint32_t w[4] = {p.q.x, p.q.y, p.q.z, p.q.w};
     const uint32_t h[4] = {p.qh.x, p.qh.y, p.qh.z, p.qh.w};
+    // Q5_K: bit c2 (c2 + 1) of every qh byte lands on bit 4 under a rotation
+    // right by c2 - 4 (c2 - 3), so one v_and_or_b32 merges it.
+    const uint32_t rl = (p.c2 + 28u) & 31u, rh = (p.c2 + 29u) & 31u;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
       if constexpr (B::kQ5) {
-        lo |= ((h[i] >> p.c2) & 0x01010101u) << 4;
-        hi |= ((h[i] >> (p.c2 + 1)) & 0x01010101u) << 4;
+        lo = and_or_b32(__builtin_amdgcn_alignbit(h[i], h[i], rl), 0x10101010u, lo);
+        hi = and_or_b32(__builtin_amdgcn_alignbit(h[i], h[i], rh), 0x10101010u, hi);
       }
       const uint4 el = x.xp[i >> 1], eh = x.xp[2 + (i >> 1)];
       a0 = dot2(wpair<kHiSub, kSel01>(lo, s.dl, s.ml), (i & 1) ? el.z : el.x, a0);
