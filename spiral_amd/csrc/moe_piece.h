@@ -127,14 +127,14 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
   uint32_t ds2;  // fp16 d (bits 0..15), sc for l < 16 (16..23), sc for l >= 16 (24..31)
   uint32_t sch;  // or-ed into ds2 bits 16..31 by prep (the streaming form loads it apart)
   int ls, hs;
-  float m0, off0, m1, off1;  // d * sc and offsets for l < 16 and l >= 16 (prep)
+  float m0, off0, m1, off1;  // d * sc and -1056 d * sc for l < 16 and l >= 16 (prep)
   __device__ __forceinline__ void prep() {
     ds2 |= sch << 16;
     const float d = fp16_scale(ds2 & 0xffffu);
     m0 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 16));
     m1 = d * static_cast<float>(static_cast<int8_t>(ds2 >> 24));
-    off0 = -32.0f * m0;
-    off1 = -32.0f * m1;
+    off0 = -1056.0f * m0;  // exact: d * sc has at most 18 significant bits, 33 has 6
+    off1 = -1056.0f * m1;
   }
   static __device__ __forceinline__ int local(int g, int s, int e) { return 32 * g + 8 * s + e; }
   // sb_row = super-block index (row * nb + sb), h = half, g = group
@@ -161,11 +161,14 @@ struct MoePiece<SPIRAL_TYPE_Q6_K> {
     uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
+      // 6-bit codes q as fp16 pairs 1024 + q: (1024 + q) ds - 1056 ds rounds
+      // (q - 32) ds once, as the single-rounded FMA of the code does.
       const uint32_t c = (((i ? wl1 : wl0) >> ls) & 0x0F0F0F0Fu) | ((((i ? wh1 : wh0) >> hs) & 0x03030303u) << 4);
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(c & 0xffu), ds, off),
-                             __builtin_fmaf(static_cast<float>((c >> 8) & 0xffu), ds, off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(static_cast<float>((c >> 16) & 0xffu), ds, off),
-                                 __builtin_fmaf(static_cast<float>(c >> 24), ds, off));
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u));
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), ds, off), __builtin_fmaf(static_cast<float>(a.y), ds, off));
+      o[2 * i + 1] =
+          pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), ds, off), __builtin_fmaf(static_cast<float>(b.y), ds, off));
     }
     return make_uint4(o[0], o[1], o[2], o[3]);
   }
@@ -181,16 +184,16 @@ template <int TYPE>
 struct MoePieceKQ {
   uint4 q, meta, qh;
   int grp;                   // 2 c
-  float d0, m0, d1, m1;      // d * scale and -dmin * min of groups 2 c and 2 c + 1 (prep)
+  float d0, m0, d1, m1;      // d * scale * 2^24 and -dmin * min of groups 2 c and 2 c + 1 (prep)
   static __device__ __forceinline__ int local(int g, int s, int e) {
     return 64 * (g >> 1) + (s < 2 ? 16 * (g & 1) + 8 * s : 32 + 16 * (g & 1) + 8 * (s - 2)) + e;
   }
   __device__ __forceinline__ void prep() {
     const uint32_t sm = kq_chunk_scales(meta.y, meta.z, meta.w, static_cast<uint32_t>(grp) >> 1);
     const float d = fp16_ieee(meta.x & 0xffffu), dm = fp16_ieee(meta.x >> 16);
-    d0 = d * static_cast<float>(sm & 0xffu);
+    d0 = d * 16777216.0f * static_cast<float>(sm & 0xffu);
     m0 = -(dm * static_cast<float>((sm >> 8) & 0xffu));
-    d1 = d * static_cast<float>((sm >> 16) & 0xffu);
+    d1 = d * 16777216.0f * static_cast<float>((sm >> 16) & 0xffu);
     m1 = -(dm * static_cast<float>(sm >> 24));
   }
   __device__ __forceinline__ void zero() { q = meta = qh = make_uint4(0u, 0u, 0u, 0u); grp = 0; }
@@ -204,10 +207,13 @@ struct MoePieceKQ {
     for (int i = 0; i < 2; ++i) {
       uint32_t c = ((i ? w1 : w0) >> (hi ? 4 : 0)) & 0x0F0F0F0Fu;
       if constexpr (TYPE == SPIRAL_TYPE_Q5_K) c |= (((i ? h1 : h0) >> (grp + (hi ? 1 : 0))) & 0x01010101u) << 4;
-      o[2 * i] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>(c & 0xffu), off),
-                             __builtin_fmaf(ds, static_cast<float>((c >> 8) & 0xffu), off));
-      o[2 * i + 1] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>((c >> 16) & 0xffu), off),
-                                 __builtin_fmaf(ds, static_cast<float>(c >> 24), off));
+      // Codes q as subnormal fp16 pairs q 2^-24 against d * scale * 2^24: the
+      // product is exact and the FMA with -dmin * min rounds once.
+      const f16x2_t a = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, c, 0x04010400u));
+      const f16x2_t b = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0u, c, 0x04030402u));
+      o[2 * i] = pack_bf16x2(__builtin_fmaf(static_cast<float>(a.x), ds, off), __builtin_fmaf(static_cast<float>(a.y), ds, off));
+      o[2 * i + 1] =
+          pack_bf16x2(__builtin_fmaf(static_cast<float>(b.x), ds, off), __builtin_fmaf(static_cast<float>(b.y), ds, off));
     }
     return make_uint4(o[0], o[1], o[2], o[3]);
   }
