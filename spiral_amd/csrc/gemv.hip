@@ -1390,8 +1390,9 @@ int launch_exact_cfg(const void* w, int64_t n_rows, int64_t k, const uint16_t* x
   return launch_status();
 }
 
-// Units of G lanes a row and J tasks a lane. Narrow groups (G < 64) serve
-// rows longer than one unit, so they keep x in LDS.
+// Units of G lanes a row and J tasks a lane. Narrow groups (G < 64) always
+// read x from LDS: rows that one narrow pass covers (16 or 32 tasks) are
+// too short for registers to matter, and it halves their instantiations.
 template <class F, int J, int G, int WAVES, int DEPTH, int MINW = 1>
 int launch_exact_j(const void* w, int64_t n_rows, int64_t k, const uint16_t* x, void* y, int y_type, hipStream_t s) {
   const int64_t T = k / F::kTaskElems;
