@@ -54,3 +54,20 @@ def test_gemv_unit_shapes(cuda, qtype, k):
     y16 = ops.mul_mat(qtype, w, N_ROWS, k, xd, out_dtype=torch.bfloat16).float().cpu().numpy()
     assert rel_err(y32, ref) <= 1e-3, rel_err(y32, ref)
     assert rel_err(y16, ref) <= 1e-2, rel_err(y16, ref)
+
+
+# The reference's first model target instantiates single-row products at
+# K = 1536 / 2048 / 4096 (src/quants/TODO.md:48-51); Q4_0 and Q8_0 are held
+# at those shapes by test_gpu_parity.py, the other formats here (K = 1536:
+# 48 tasks, rows in 16-lane groups).
+@pytest.mark.parametrize("qtype", [O.Q6_K, O.Q4_K, O.Q5_K, O.IQ4_NL, O.IQ4_XS])
+@pytest.mark.parametrize("k", (1536, 2048, 4096))
+@pytest.mark.parametrize("n", (2048, 12288))
+def test_gemv_model_shapes(cuda, qtype, k, n):
+    raw = synth.make_weights(qtype, n, k, 700 + n + k)
+    x = synth.make_x(1, k, 800 + k)
+    w = ops.to_planar(qtype, torch.from_numpy(raw).to(cuda), n, k)
+    xd = torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).to(cuda)
+    y32 = ops.mul_mat(qtype, w, n, k, xd, out_dtype=torch.float32).cpu().numpy()
+    ref = O.matmul_f64(O.dequant(qtype, raw, n, k), x)
+    assert rel_err(y32, ref) <= 1e-3, rel_err(y32, ref)
